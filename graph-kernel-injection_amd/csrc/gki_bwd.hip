@@ -1,0 +1,682 @@
+// Block-sparse StreamingLLM attention: backward kernels for gfx950.
+//
+// Replaces the reference's three Triton launches in
+// `_BlockSparseFlashAttention.backward` (sparse_triton_kernel.py:719-777):
+//   * delta_kernel  <- `_bwd_preprocess_kernel` (sparse_triton_kernel.py:354-392):
+//       Delta[q] = sum_d fp32(O) * fp32(dO), using the stored O.
+//   * dkdv_kernel   <- `_bwd_dkdv_kernel` (sparse_triton_kernel.py:394-509):
+//       one workgroup per 64-row KV tile, loop over the kept q tiles of its
+//       column (CSC list), P = exp(S - LSE), dV += P^T dO, dS = P (dP - Delta)
+//       * scale, dK += dS^T Q. No atomics; one store per tile.
+//   * dq_kernel     <- `_bwd_dq_kernel` (sparse_triton_kernel.py:511-601):
+//       one workgroup per 64-row q tile, loop over its kept kv tiles (CSR),
+//       dQ += dS K.
+// Casts follow the reference: P^T -> dO dtype for dV, dS -> Q/K dtype for
+// dK/dQ, results stored in the input dtype.
+//
+// MI355X specifics: the KV-tile grid is ordered "heavy columns first" (the sink
+// column is kept by every q tile, so it runs longest); the remaining tiles are
+// XCD-remapped so neighbouring tiles of one head share L2.
+#include "gki_common.cuh"
+
+namespace gki {
+namespace {
+
+// ---------------------------------------------------------------------------
+// Delta = rowsum(O * dO)
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+__global__ __launch_bounds__(256) void delta_kernel(const typename T::storage* __restrict__ O,
+                                                    const typename T::storage* __restrict__ dO,
+                                                    float* __restrict__ delta, int64_t rows) {
+  constexpr int VEC = T::is_f32 ? 4 : 8;
+  constexpr int LPR = D / VEC;          // lanes per row (2..32)
+  constexpr int RPB = 256 / LPR;        // rows per block
+  const int tid = threadIdx.x;
+  const int64_t row = (int64_t)blockIdx.x * RPB + tid / LPR;
+  const int ch = tid % LPR;
+  float acc = 0.f;
+  if (row < rows) {
+    const uint4 a = *(const uint4*)(O + row * D + ch * VEC);
+    const uint4 b = *(const uint4*)(dO + row * D + ch * VEC);
+    if constexpr (T::is_f32) {
+      const float* fa = (const float*)&a;
+      const float* fb = (const float*)&b;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc += fa[i] * fb[i];
+    } else {
+      const uint16_t* ha = (const uint16_t*)&a;
+      const uint16_t* hb = (const uint16_t*)&b;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc += T::to_float(ha[i]) * T::to_float(hb[i]);
+    }
+  }
+#pragma unroll
+  for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+  if (row < rows && ch == 0) delta[row] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// Shared staging: a 64-row tile of a [n, D] 16-bit matrix into LDS, both
+// row-major (stride D+8) and transposed (XOR-swizzled 8-element chunks), from a
+// register prefetch. Task (rg, ch) covers rows 4rg..4rg+3, columns 8ch..8ch+7.
+// ---------------------------------------------------------------------------
+template <int D>
+struct Stage16 {
+  static constexpr int LD = D + 8;
+  static constexpr int CPR = D / 8;
+  static constexpr int TASKS = 16 * CPR;
+  static constexpr int P = (TASKS + 255) / 256;
+  uint4 reg[P][4];
+
+  __device__ inline void load(const uint16_t* base, int r0, int n_rows, int tid) {
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int task = tid + 256 * p;
+      const int rg = task & 15, ch = task >> 4;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = r0 + 4 * rg + r;
+        reg[p][r] = (task < TASKS && row < n_rows) ? *(const uint4*)(base + (size_t)row * D + ch * 8)
+                                                   : make_uint4(0, 0, 0, 0);
+      }
+    }
+  }
+  __device__ inline void store(uint16_t* rowmajor, uint16_t* transposed, int tid) const {
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int task = tid + 256 * p;
+      if (task >= TASKS) continue;
+      const int rg = task & 15, ch = task >> 4;
+      if (rowmajor) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) *(uint4*)(&rowmajor[(4 * rg + r) * LD + ch * 8]) = reg[p][r];
+      }
+      if (transposed) {
+        const uint16_t* e0 = (const uint16_t*)&reg[p][0];
+        const uint16_t* e1 = (const uint16_t*)&reg[p][1];
+        const uint16_t* e2 = (const uint16_t*)&reg[p][2];
+        const uint16_t* e3 = (const uint16_t*)&reg[p][3];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int d = ch * 8 + j;
+          const int phys = (((rg >> 1) ^ (d & 7)) << 3) + ((rg & 1) << 2);
+          uint2 w;
+          w.x = (uint32_t)e0[j] | ((uint32_t)e1[j] << 16);
+          w.y = (uint32_t)e2[j] | ((uint32_t)e3[j] << 16);
+          *(uint2*)(&transposed[d * 64 + phys]) = w;
+        }
+      }
+    }
+  }
+};
+// Read the 8 contiguous elements [c8*8, c8*8+8) of transposed row d.
+__device__ inline uint4 ldsT(const uint16_t* transposed, int d, int c8) {
+  return *(const uint4*)(&transposed[d * 64 + ((c8 ^ (d & 7)) << 3)]);
+}
+
+template <int D>
+struct Stage32 {
+  static constexpr int LD = D + 4;
+  static constexpr int CPR = D / 4;
+  static constexpr int CH = 64 * CPR;
+  static constexpr int P = (CH + 255) / 256;
+  float4 reg[P];
+  __device__ inline void load(const float* base, int r0, int n_rows, int tid) {
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int c = tid + 256 * p;
+      const int r = c / CPR, ch = c - r * CPR;
+      reg[p] = (c < CH && r0 + r < n_rows) ? *(const float4*)(base + (size_t)(r0 + r) * D + ch * 4)
+                                           : make_float4(0, 0, 0, 0);
+    }
+  }
+  __device__ inline void store(float* rowmajor, int tid) const {
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int c = tid + 256 * p;
+      if (c < CH) {
+        const int r = c / CPR, ch = c - r * CPR;
+        *(float4*)(&rowmajor[r * LD + ch * 4]) = reg[p];
+      }
+    }
+  }
+};
+
+// Workgroup -> (bh, kv tile) for the dK/dV grid: the first n_heavy*BH blocks
+// take the heavy columns (spread round-robin over XCDs so they start first),
+// the rest walk each head's remaining columns in order, XCD-remapped.
+__device__ inline void dkdv_tile_of(int b, int BH, int n_kt, int n_heavy, const int32_t* order,
+                                    int& bh, int& kt) {
+  if (b < n_heavy * BH) {
+    bh = b % BH;
+    kt = order[b / BH];
+  } else {
+    const int n_rest = n_kt - n_heavy;
+    const int b2 = b - n_heavy * BH;
+    const int L = xcd_remap(b2, n_rest * BH);
+    bh = L / n_rest;
+    kt = order[n_heavy + (L - bh * n_rest)];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dK / dV, 16-bit
+// ---------------------------------------------------------------------------
+template <int D>
+struct DkdvSmem16 {
+  uint16_t q[64 * (D + 8)];
+  uint16_t qt[D * 64];
+  uint16_t dout[64 * (D + 8)];
+  uint16_t dot[D * 64];
+  float lse2[64];
+  float dlt[64];
+};
+
+template <typename T, int D>
+__global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
+    Geom g, const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+    const uint16_t* __restrict__ V, const uint16_t* __restrict__ dO, uint16_t* __restrict__ dK,
+    uint16_t* __restrict__ dV, const float* __restrict__ LSE, const float* __restrict__ Delta,
+    const int32_t* __restrict__ col_ptr, const int32_t* __restrict__ col_idx,
+    const int32_t* __restrict__ order, int n_heavy, int n_kt) {
+  constexpr int KS = (D + 31) / 32;
+  constexpr int DT = D / 16;
+  constexpr int LD = D + 8;
+  __shared__ DkdvSmem16<D> sm;
+  Stage16<D> sq, sdo;
+
+  const int BH = g.B * g.H;
+  int bh, kt;
+  dkdv_tile_of(blockIdx.x, BH, n_kt, n_heavy, order, bh, kt);
+  const size_t qb = (size_t)bh * g.n_q * D;
+  const size_t kb = (size_t)bh * g.n_kv * D;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int grp = lane >> 4, col = lane & 15;
+  const int k_w = kt * kTileN + wave * 16;
+  const int my_kv = k_w + col;
+
+  uint4 kf[KS], vf[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const int d0 = 32 * ks + 8 * grp;
+    const bool ok = my_kv < g.n_kv && d0 < D;
+    kf[ks] = ok ? *(const uint4*)(K + kb + (size_t)my_kv * D + d0) : make_uint4(0, 0, 0, 0);
+    vf[ks] = ok ? *(const uint4*)(V + kb + (size_t)my_kv * D + d0) : make_uint4(0, 0, 0, 0);
+  }
+  floatx4 dk[DT], dv[DT];
+#pragma unroll
+  for (int i = 0; i < DT; ++i) dk[i] = dv[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  const int e_beg = col_ptr[kt], e_end = col_ptr[kt + 1];
+  float lreg = 0.f, dreg = 0.f;
+  auto load_tile = [&](int q0) {
+    sq.load(Q + qb, q0, g.n_q, tid);
+    sdo.load(dO + qb, q0, g.n_q, tid);
+    if (tid < 64) {
+      const int r = q0 + tid;
+      lreg = r < g.n_q ? LSE[(size_t)bh * g.n_q + r] * kLog2e : 0.f;
+      dreg = r < g.n_q ? Delta[(size_t)bh * g.n_q + r] : 0.f;
+    }
+  };
+  if (e_beg < e_end) load_tile((col_idx[e_beg] & kIdxMask) * kTileM);
+
+  const int kv_hi_wave = min(k_w + 15, g.n_kv - 1);
+  for (int e = e_beg; e < e_end; ++e) {
+    const int ent = col_idx[e];
+    const int q0 = (ent & kIdxMask) * kTileM;
+    const bool partial = (ent >> kPartialBit) & 1;
+    __syncthreads();
+    sq.store(sm.q, sm.qt, tid);
+    sdo.store(sm.dout, sm.dot, tid);
+    if (tid < 64) {
+      sm.lse2[tid] = lreg;
+      sm.dlt[tid] = dreg;
+    }
+    __syncthreads();
+    if (e + 1 < e_end) load_tile((col_idx[e + 1] & kIdxMask) * kTileM);
+
+    const bool need_mask = partial || (q0 + kTileM > g.n_q) || (k_w + 15 >= g.n_kv) ||
+                           !tile_all_visible(g, q0, min(q0 + kTileM - 1, g.n_q - 1), k_w, kv_hi_wave);
+    // S and dP for the four 16-row q subtiles (rows rho(t, .)).
+    floatx4 p[4], ds[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
+      floatx4 dp = floatx4{0.f, 0.f, 0.f, 0.f};
+      const int r = rho(t, col);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int d0 = 32 * ks + 8 * grp;
+        const uint4 aq = (d0 < D) ? *(const uint4*)(&sm.q[r * LD + d0]) : make_uint4(0, 0, 0, 0);
+        const uint4 ad = (d0 < D) ? *(const uint4*)(&sm.dout[r * LD + d0]) : make_uint4(0, 0, 0, 0);
+        s = T::mfma(aq, kf[ks], s);
+        dp = T::mfma(ad, vf[ks], dp);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int qr = rho(t, 4 * grp + i);
+        float pv = __builtin_amdgcn_exp2f(s[i] * g.scale_log2 - sm.lse2[qr]);
+        if (need_mask && !elem_valid(g, q0 + qr, my_kv, partial)) pv = 0.f;
+        p[t][i] = pv;
+        ds[t][i] = pv * (dp[i] - sm.dlt[qr]) * g.scale;
+      }
+    }
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      float pa[8] = {p[2 * st][0], p[2 * st][1], p[2 * st][2], p[2 * st][3],
+                     p[2 * st + 1][0], p[2 * st + 1][1], p[2 * st + 1][2], p[2 * st + 1][3]};
+      float da[8] = {ds[2 * st][0], ds[2 * st][1], ds[2 * st][2], ds[2 * st][3],
+                     ds[2 * st + 1][0], ds[2 * st + 1][1], ds[2 * st + 1][2], ds[2 * st + 1][3]};
+      const uint4 ap = pack8<T>(pa);
+      const uint4 ad = pack8<T>(da);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const int d = 16 * dt + col;
+        dv[dt] = T::mfma(ap, ldsT(sm.dot, d, 4 * st + grp), dv[dt]);
+        dk[dt] = T::mfma(ad, ldsT(sm.qt, d, 4 * st + grp), dk[dt]);
+      }
+    }
+  }
+
+  // dK/dV accumulators: lane holds rows k_w + 4grp + i, column 16dt + col.
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = k_w + 4 * grp + i;
+    if (row < g.n_kv) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        dK[kb + (size_t)row * D + 16 * dt + col] = T::from_float(dk[dt][i]);
+        dV[kb + (size_t)row * D + 16 * dt + col] = T::from_float(dv[dt][i]);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dK / dV, fp32
+// ---------------------------------------------------------------------------
+template <int D>
+struct DkdvSmem32 {
+  float q[64 * (D + 4)];
+  float dout[64 * (D + 4)];
+  float lse2[64];
+  float dlt[64];
+};
+
+template <int D>
+__global__ __launch_bounds__(256, 2) void dkdv_kernel_32(
+    Geom g, const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+    const float* __restrict__ dO, float* __restrict__ dK, float* __restrict__ dV,
+    const float* __restrict__ LSE, const float* __restrict__ Delta,
+    const int32_t* __restrict__ col_ptr, const int32_t* __restrict__ col_idx,
+    const int32_t* __restrict__ order, int n_heavy, int n_kt) {
+  constexpr int KS = D / 4;
+  constexpr int DT = D / 16;
+  constexpr int LD = D + 4;
+  __shared__ DkdvSmem32<D> sm;
+  Stage32<D> sq, sdo;
+
+  const int BH = g.B * g.H;
+  int bh, kt;
+  dkdv_tile_of(blockIdx.x, BH, n_kt, n_heavy, order, bh, kt);
+  const size_t qb = (size_t)bh * g.n_q * D;
+  const size_t kb = (size_t)bh * g.n_kv * D;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int grp = lane >> 4, col = lane & 15;
+  const int k_w = kt * kTileN + wave * 16;
+  const int my_kv = k_w + col;
+
+  float kf[KS], vf[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const bool ok = my_kv < g.n_kv;
+    kf[ks] = ok ? K[kb + (size_t)my_kv * D + 4 * ks + grp] : 0.f;
+    vf[ks] = ok ? V[kb + (size_t)my_kv * D + 4 * ks + grp] : 0.f;
+  }
+  floatx4 dk[DT], dv[DT];
+#pragma unroll
+  for (int i = 0; i < DT; ++i) dk[i] = dv[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  const int e_beg = col_ptr[kt], e_end = col_ptr[kt + 1];
+  float lreg = 0.f, dreg = 0.f;
+  auto load_tile = [&](int q0) {
+    sq.load(Q + qb, q0, g.n_q, tid);
+    sdo.load(dO + qb, q0, g.n_q, tid);
+    if (tid < 64) {
+      const int r = q0 + tid;
+      lreg = r < g.n_q ? LSE[(size_t)bh * g.n_q + r] * kLog2e : 0.f;
+      dreg = r < g.n_q ? Delta[(size_t)bh * g.n_q + r] : 0.f;
+    }
+  };
+  if (e_beg < e_end) load_tile((col_idx[e_beg] & kIdxMask) * kTileM);
+
+  const int kv_hi_wave = min(k_w + 15, g.n_kv - 1);
+  for (int e = e_beg; e < e_end; ++e) {
+    const int ent = col_idx[e];
+    const int q0 = (ent & kIdxMask) * kTileM;
+    const bool partial = (ent >> kPartialBit) & 1;
+    __syncthreads();
+    sq.store(sm.q, tid);
+    sdo.store(sm.dout, tid);
+    if (tid < 64) {
+      sm.lse2[tid] = lreg;
+      sm.dlt[tid] = dreg;
+    }
+    __syncthreads();
+    if (e + 1 < e_end) load_tile((col_idx[e + 1] & kIdxMask) * kTileM);
+
+    const bool need_mask = partial || (q0 + kTileM > g.n_q) || (k_w + 15 >= g.n_kv) ||
+                           !tile_all_visible(g, q0, min(q0 + kTileM - 1, g.n_q - 1), k_w, kv_hi_wave);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
+      floatx4 dp = floatx4{0.f, 0.f, 0.f, 0.f};
+      const int r = rho(t, col);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        s = mfma_f32(sm.q[r * LD + 4 * ks + grp], kf[ks], s);
+        dp = mfma_f32(sm.dout[r * LD + 4 * ks + grp], vf[ks], dp);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int qr = rho(t, 4 * grp + i);
+        float pv = __builtin_amdgcn_exp2f(s[i] * g.scale_log2 - sm.lse2[qr]);
+        if (need_mask && !elem_valid(g, q0 + qr, my_kv, partial)) pv = 0.f;
+        const float dsv = pv * (dp[i] - sm.dlt[qr]) * g.scale;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          dv[dt] = mfma_f32(pv, sm.dout[qr * LD + 16 * dt + col], dv[dt]);
+          dk[dt] = mfma_f32(dsv, sm.q[qr * LD + 16 * dt + col], dk[dt]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = k_w + 4 * grp + i;
+    if (row < g.n_kv) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        dK[kb + (size_t)row * D + 16 * dt + col] = dk[dt][i];
+        dV[kb + (size_t)row * D + 16 * dt + col] = dv[dt][i];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dQ, 16-bit
+// ---------------------------------------------------------------------------
+template <int D>
+struct DqSmem16 {
+  uint16_t k[64 * (D + 8)];
+  uint16_t kt[D * 64];
+  uint16_t v[64 * (D + 8)];
+};
+
+template <typename T, int D>
+__global__ __launch_bounds__(256, 2) void dq_kernel_16(
+    Geom g, const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+    const uint16_t* __restrict__ V, const uint16_t* __restrict__ dO, uint16_t* __restrict__ dQ,
+    const float* __restrict__ LSE, const float* __restrict__ Delta,
+    const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ row_idx, int n_qt) {
+  constexpr int KS = (D + 31) / 32;
+  constexpr int DT = D / 16;
+  constexpr int LD = D + 8;
+  __shared__ DqSmem16<D> sm;
+  Stage16<D> sk, sv;
+
+  const int n_wg = n_qt * g.B * g.H;
+  const int wg = xcd_remap(blockIdx.x, n_wg);
+  const int bh = wg / n_qt, qt = wg - bh * n_qt;
+  const size_t qb = (size_t)bh * g.n_q * D;
+  const size_t kb = (size_t)bh * g.n_kv * D;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int grp = lane >> 4, col = lane & 15;
+  const int q0 = qt * kTileM + wave * 16;
+  const int my_q = q0 + col;
+
+  uint4 qf[KS], df[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const int d0 = 32 * ks + 8 * grp;
+    const bool ok = my_q < g.n_q && d0 < D;
+    qf[ks] = ok ? *(const uint4*)(Q + qb + (size_t)my_q * D + d0) : make_uint4(0, 0, 0, 0);
+    df[ks] = ok ? *(const uint4*)(dO + qb + (size_t)my_q * D + d0) : make_uint4(0, 0, 0, 0);
+  }
+  const float lse2 = my_q < g.n_q ? LSE[(size_t)bh * g.n_q + my_q] * kLog2e : 0.f;
+  const float dlt = my_q < g.n_q ? Delta[(size_t)bh * g.n_q + my_q] : 0.f;
+
+  floatx4 dq[DT];
+#pragma unroll
+  for (int i = 0; i < DT; ++i) dq[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  const int e_beg = row_ptr[qt], e_end = row_ptr[qt + 1];
+  if (e_beg < e_end) {
+    const int k0 = (row_idx[e_beg] & kIdxMask) * kTileN;
+    sk.load(K + kb, k0, g.n_kv, tid);
+    sv.load(V + kb, k0, g.n_kv, tid);
+  }
+  const int q_hi_wave = min(q0 + 15, g.n_q - 1);
+  for (int e = e_beg; e < e_end; ++e) {
+    const int ent = row_idx[e];
+    const int k0 = (ent & kIdxMask) * kTileN;
+    const bool partial = (ent >> kPartialBit) & 1;
+    __syncthreads();
+    sk.store(sm.k, sm.kt, tid);
+    sv.store(sm.v, nullptr, tid);
+    __syncthreads();
+    if (e + 1 < e_end) {
+      const int k1 = (row_idx[e + 1] & kIdxMask) * kTileN;
+      sk.load(K + kb, k1, g.n_kv, tid);
+      sv.load(V + kb, k1, g.n_kv, tid);
+    }
+    const bool need_mask = partial || (q0 + 15 >= g.n_q) || (k0 + kTileN > g.n_kv) ||
+                           !tile_all_visible(g, q0, q_hi_wave, k0, k0 + kTileN - 1);
+    floatx4 ds[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
+      floatx4 dp = floatx4{0.f, 0.f, 0.f, 0.f};
+      const int r = rho(t, col);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int d0 = 32 * ks + 8 * grp;
+        const uint4 ak = (d0 < D) ? *(const uint4*)(&sm.k[r * LD + d0]) : make_uint4(0, 0, 0, 0);
+        const uint4 av = (d0 < D) ? *(const uint4*)(&sm.v[r * LD + d0]) : make_uint4(0, 0, 0, 0);
+        s = T::mfma(ak, qf[ks], s);
+        dp = T::mfma(av, df[ks], dp);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float pv = __builtin_amdgcn_exp2f(s[i] * g.scale_log2 - lse2);
+        if (need_mask && !elem_valid(g, my_q, k0 + rho(t, 4 * grp + i), partial)) pv = 0.f;
+        ds[t][i] = pv * (dp[i] - dlt) * g.scale;
+      }
+    }
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      float da[8] = {ds[2 * st][0], ds[2 * st][1], ds[2 * st][2], ds[2 * st][3],
+                     ds[2 * st + 1][0], ds[2 * st + 1][1], ds[2 * st + 1][2], ds[2 * st + 1][3]};
+      const uint4 b = pack8<T>(da);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) dq[dt] = T::mfma(ldsT(sm.kt, 16 * dt + col, 4 * st + grp), b, dq[dt]);
+    }
+  }
+  if (my_q < g.n_q) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      uint2 w;
+      w.x = (uint32_t)T::from_float(dq[dt][0]) | ((uint32_t)T::from_float(dq[dt][1]) << 16);
+      w.y = (uint32_t)T::from_float(dq[dt][2]) | ((uint32_t)T::from_float(dq[dt][3]) << 16);
+      *(uint2*)(dQ + qb + (size_t)my_q * D + 16 * dt + 4 * grp) = w;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dQ, fp32
+// ---------------------------------------------------------------------------
+template <int D>
+struct DqSmem32 {
+  float k[64 * (D + 4)];
+  float v[64 * (D + 4)];
+};
+
+template <int D>
+__global__ __launch_bounds__(256, 2) void dq_kernel_32(
+    Geom g, const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+    const float* __restrict__ dO, float* __restrict__ dQ, const float* __restrict__ LSE,
+    const float* __restrict__ Delta, const int32_t* __restrict__ row_ptr,
+    const int32_t* __restrict__ row_idx, int n_qt) {
+  constexpr int KS = D / 4;
+  constexpr int DT = D / 16;
+  constexpr int LD = D + 4;
+  __shared__ DqSmem32<D> sm;
+  Stage32<D> sk, sv;
+
+  const int n_wg = n_qt * g.B * g.H;
+  const int wg = xcd_remap(blockIdx.x, n_wg);
+  const int bh = wg / n_qt, qt = wg - bh * n_qt;
+  const size_t qb = (size_t)bh * g.n_q * D;
+  const size_t kb = (size_t)bh * g.n_kv * D;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int grp = lane >> 4, col = lane & 15;
+  const int q0 = qt * kTileM + wave * 16;
+  const int my_q = q0 + col;
+
+  float qf[KS], df[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const bool ok = my_q < g.n_q;
+    qf[ks] = ok ? Q[qb + (size_t)my_q * D + 4 * ks + grp] : 0.f;
+    df[ks] = ok ? dO[qb + (size_t)my_q * D + 4 * ks + grp] : 0.f;
+  }
+  const float lse2 = my_q < g.n_q ? LSE[(size_t)bh * g.n_q + my_q] * kLog2e : 0.f;
+  const float dlt = my_q < g.n_q ? Delta[(size_t)bh * g.n_q + my_q] : 0.f;
+  floatx4 dq[DT];
+#pragma unroll
+  for (int i = 0; i < DT; ++i) dq[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  const int e_beg = row_ptr[qt], e_end = row_ptr[qt + 1];
+  if (e_beg < e_end) {
+    const int k0 = (row_idx[e_beg] & kIdxMask) * kTileN;
+    sk.load(K + kb, k0, g.n_kv, tid);
+    sv.load(V + kb, k0, g.n_kv, tid);
+  }
+  const int q_hi_wave = min(q0 + 15, g.n_q - 1);
+  for (int e = e_beg; e < e_end; ++e) {
+    const int ent = row_idx[e];
+    const int k0 = (ent & kIdxMask) * kTileN;
+    const bool partial = (ent >> kPartialBit) & 1;
+    __syncthreads();
+    sk.store(sm.k, tid);
+    sv.store(sm.v, tid);
+    __syncthreads();
+    if (e + 1 < e_end) {
+      const int k1 = (row_idx[e + 1] & kIdxMask) * kTileN;
+      sk.load(K + kb, k1, g.n_kv, tid);
+      sv.load(V + kb, k1, g.n_kv, tid);
+    }
+    const bool need_mask = partial || (q0 + 15 >= g.n_q) || (k0 + kTileN > g.n_kv) ||
+                           !tile_all_visible(g, q0, q_hi_wave, k0, k0 + kTileN - 1);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
+      floatx4 dp = floatx4{0.f, 0.f, 0.f, 0.f};
+      const int r = rho(t, col);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        s = mfma_f32(sm.k[r * LD + 4 * ks + grp], qf[ks], s);
+        dp = mfma_f32(sm.v[r * LD + 4 * ks + grp], df[ks], dp);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int kr = rho(t, 4 * grp + i);
+        float pv = __builtin_amdgcn_exp2f(s[i] * g.scale_log2 - lse2);
+        if (need_mask && !elem_valid(g, my_q, k0 + kr, partial)) pv = 0.f;
+        const float dsv = pv * (dp[i] - dlt) * g.scale;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) dq[dt] = mfma_f32(sm.k[kr * LD + 16 * dt + col], dsv, dq[dt]);
+      }
+    }
+  }
+  if (my_q < g.n_q) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      float4 w = make_float4(dq[dt][0], dq[dt][1], dq[dt][2], dq[dt][3]);
+      *(float4*)(dQ + qb + (size_t)my_q * D + 16 * dt + 4 * grp) = w;
+    }
+  }
+}
+
+template <typename T, int D>
+void launch_delta(const void* o, const void* dout, float* delta, int64_t rows, hipStream_t stream) {
+  constexpr int VEC = T::is_f32 ? 4 : 8;
+  constexpr int RPB = 256 / (D / VEC);
+  const int64_t grid = (rows + RPB - 1) / RPB;
+  hipLaunchKernelGGL((delta_kernel<T, D>), dim3((unsigned)grid), dim3(256), 0, stream,
+                     (const typename T::storage*)o, (const typename T::storage*)dout, delta, rows);
+}
+
+template <int D>
+int launch_bwd(int dtype, const Geom& g, const void* q, const void* k, const void* v, const void* o,
+               const void* dout, const float* lse, void* dq, void* dk, void* dv, float* delta,
+               const int32_t* row_ptr, const int32_t* row_idx, int n_qt, const int32_t* col_ptr,
+               const int32_t* col_idx, const int32_t* order, int n_heavy, int n_kt,
+               hipStream_t stream) {
+  const int BH = g.B * g.H;
+  const int64_t rows = (int64_t)BH * g.n_q;
+  if (dtype == kF32) {
+    launch_delta<F32, D>(o, dout, delta, rows, stream);
+    hipLaunchKernelGGL(dkdv_kernel_32<D>, dim3(n_kt * BH), dim3(256), 0, stream, g, (const float*)q,
+                       (const float*)k, (const float*)v, (const float*)dout, (float*)dk, (float*)dv,
+                       lse, delta, col_ptr, col_idx, order, n_heavy, n_kt);
+    hipLaunchKernelGGL(dq_kernel_32<D>, dim3(n_qt * BH), dim3(256), 0, stream, g, (const float*)q,
+                       (const float*)k, (const float*)v, (const float*)dout, (float*)dq, lse, delta,
+                       row_ptr, row_idx, n_qt);
+  } else if (dtype == kF16) {
+    launch_delta<F16, D>(o, dout, delta, rows, stream);
+    hipLaunchKernelGGL((dkdv_kernel_16<F16, D>), dim3(n_kt * BH), dim3(256), 0, stream, g,
+                       (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
+                       (const uint16_t*)dout, (uint16_t*)dk, (uint16_t*)dv, lse, delta, col_ptr,
+                       col_idx, order, n_heavy, n_kt);
+    hipLaunchKernelGGL((dq_kernel_16<F16, D>), dim3(n_qt * BH), dim3(256), 0, stream, g,
+                       (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
+                       (const uint16_t*)dout, (uint16_t*)dq, lse, delta, row_ptr, row_idx, n_qt);
+  } else {
+    launch_delta<BF16, D>(o, dout, delta, rows, stream);
+    hipLaunchKernelGGL((dkdv_kernel_16<BF16, D>), dim3(n_kt * BH), dim3(256), 0, stream, g,
+                       (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
+                       (const uint16_t*)dout, (uint16_t*)dk, (uint16_t*)dv, lse, delta, col_ptr,
+                       col_idx, order, n_heavy, n_kt);
+    hipLaunchKernelGGL((dq_kernel_16<BF16, D>), dim3(n_qt * BH), dim3(256), 0, stream, g,
+                       (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
+                       (const uint16_t*)dout, (uint16_t*)dq, lse, delta, row_ptr, row_idx, n_qt);
+  }
+  return check_launch("gki_bsa_bwd");
+}
+
+}  // namespace
+
+int bwd_dispatch(int dtype, int head_dim, const Geom& g, const void* q, const void* k, const void* v,
+                 const void* o, const void* dout, const float* lse, void* dq, void* dk, void* dv,
+                 float* delta, const int32_t* row_ptr, const int32_t* row_idx, int n_qt,
+                 const int32_t* col_ptr, const int32_t* col_idx, const int32_t* order, int n_heavy,
+                 int n_kt, hipStream_t stream) {
+#define GKI_BWD_CASE(DD)                                                                          \
+  case DD:                                                                                        \
+    return launch_bwd<DD>(dtype, g, q, k, v, o, dout, lse, dq, dk, dv, delta, row_ptr, row_idx,   \
+                          n_qt, col_ptr, col_idx, order, n_heavy, n_kt, stream);
+  switch (head_dim) {
+    GKI_BWD_CASE(16)
+    GKI_BWD_CASE(32)
+    GKI_BWD_CASE(64)
+    GKI_BWD_CASE(128)
+    default: return fail(2, "unsupported head_dim " + std::to_string(head_dim));
+  }
+#undef GKI_BWD_CASE
+}
+
+}  // namespace gki

@@ -1,0 +1,155 @@
+// C ABI of the block-sparse attention library (declared in include/gki_bsa.h).
+//
+// Every entry point is stateless and asynchronous on the caller's stream: it
+// validates its arguments, launches, and returns 0 or a non-zero code whose
+// message is available from gki_last_error() (thread-local). The library never
+// allocates or frees device memory and keeps no pointer after returning.
+#include "gki_common.cuh"
+
+namespace gki {
+
+namespace {
+thread_local std::string g_last_error;
+}
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+int check_launch(const char* what) {
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return fail(3, std::string(what) + ": " + hipGetErrorString(err));
+  return 0;
+}
+
+int fwd_dispatch(int dtype, int head_dim, const Geom& g, const void* q, const void* k, const void* v,
+                 void* o, float* lse, const int32_t* row_ptr, const int32_t* row_idx, int n_qt,
+                 hipStream_t stream);
+int bwd_dispatch(int dtype, int head_dim, const Geom& g, const void* q, const void* k, const void* v,
+                 const void* o, const void* dout, const float* lse, void* dq, void* dk, void* dv,
+                 float* delta, const int32_t* row_ptr, const int32_t* row_idx, int n_qt,
+                 const int32_t* col_ptr, const int32_t* col_idx, const int32_t* order, int n_heavy,
+                 int n_kt, hipStream_t stream);
+int decode_dispatch(int dtype, int head_dim, const Geom& g, const void* q, const void* k, const void* v,
+                    void* o, float* lse, const int32_t* list, int n_ent, float* ws, int n_splits,
+                    hipStream_t stream);
+int decode_max_tokens_per_split();
+
+namespace {
+
+int make_geom(Geom& g, int dtype, int B, int H, int n_q, int n_kv, int head_dim, const int32_t* mask,
+              int n_qb, int n_kb, int block_m, int block_n, float scale, int causal, int sink,
+              int window) {
+  GKI_REQUIRE(dtype == kF32 || dtype == kF16 || dtype == kBF16, 2,
+              "unsupported dtype code " + std::to_string(dtype) + " (0=fp32, 1=fp16, 2=bf16)");
+  GKI_REQUIRE(head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128, 2,
+              "unsupported head_dim " + std::to_string(head_dim) + " (supported: 16, 32, 64, 128)");
+  GKI_REQUIRE(B > 0 && H > 0 && n_q > 0 && n_kv > 0, 1, "B, H, n_q and n_kv must be positive");
+  GKI_REQUIRE(block_m > 0 && block_n > 0, 1, "block_m and block_n must be positive");
+  GKI_REQUIRE(n_qb == (n_q + block_m - 1) / block_m && n_kb == (n_kv + block_n - 1) / block_n, 1,
+              "block mask shape does not match ceil(n_q/block_m) x ceil(n_kv/block_n)");
+  GKI_REQUIRE(sink >= 0 && window >= 0, 1, "sink_size and window_size must be non-negative");
+  GKI_REQUIRE((int64_t)n_kv < (1ll << kPartialBit), 1, "n_kv too large");
+  GKI_REQUIRE(mask != nullptr, 1, "null block mask");
+  g.B = B;
+  g.H = H;
+  g.n_q = n_q;
+  g.n_kv = n_kv;
+  g.q_off = n_kv - n_q;
+  g.scale = scale;
+  g.scale_log2 = scale * kLog2e;
+  g.causal = causal ? 1 : 0;
+  g.sink = sink;
+  g.window = window;
+  g.mask = mask;
+  g.n_qb = n_qb;
+  g.n_kb = n_kb;
+  g.bm = block_m;
+  g.bn = block_n;
+  return 0;
+}
+
+}  // namespace
+}  // namespace gki
+
+using namespace gki;
+
+extern "C" {
+
+int gki_abi_version(void) { return 1; }
+
+const char* gki_last_error(void) { return g_last_error.c_str(); }
+
+int gki_tile_sizes(int32_t* tile_m, int32_t* tile_n, int32_t* decode_tile_m, int32_t* decode_max_q,
+                   int32_t* decode_max_tokens) {
+  if (tile_m) *tile_m = kTileM;
+  if (tile_n) *tile_n = kTileN;
+  if (decode_tile_m) *decode_tile_m = kDecodeTileM;
+  if (decode_max_q) *decode_max_q = kDecodeMaxQ;
+  if (decode_max_tokens) *decode_max_tokens = decode_max_tokens_per_split();
+  return 0;
+}
+
+int gki_bsa_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int32_t dtype,
+                int32_t B, int32_t H, int32_t n_q, int32_t n_kv, int32_t head_dim,
+                const int32_t* row_ptr, const int32_t* row_idx, int32_t n_qt, const int32_t* mask,
+                int32_t n_qb, int32_t n_kb, int32_t block_m, int32_t block_n, float softmax_scale,
+                int32_t is_causal, int32_t sink_size, int32_t window_size, void* stream) {
+  Geom g;
+  if (int rc = make_geom(g, dtype, B, H, n_q, n_kv, head_dim, mask, n_qb, n_kb, block_m, block_n,
+                         softmax_scale, is_causal, sink_size, window_size))
+    return rc;
+  GKI_REQUIRE(q && k && v && o && lse && row_ptr && row_idx, 1, "gki_bsa_fwd: null pointer");
+  GKI_REQUIRE(n_qt == (n_q + kTileM - 1) / kTileM, 1, "gki_bsa_fwd: schedule row count mismatch");
+  return fwd_dispatch(dtype, head_dim, g, q, k, v, o, lse, row_ptr, row_idx, n_qt, (hipStream_t)stream);
+}
+
+int gki_bsa_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                const float* lse, void* dq, void* dk, void* dv, float* delta, int32_t dtype, int32_t B,
+                int32_t H, int32_t n_q, int32_t n_kv, int32_t head_dim, const int32_t* row_ptr,
+                const int32_t* row_idx, int32_t n_qt, const int32_t* col_ptr, const int32_t* col_idx,
+                const int32_t* kv_order, int32_t n_heavy, int32_t n_kt, const int32_t* mask,
+                int32_t n_qb, int32_t n_kb, int32_t block_m, int32_t block_n, float softmax_scale,
+                int32_t is_causal, int32_t sink_size, int32_t window_size, void* stream) {
+  Geom g;
+  if (int rc = make_geom(g, dtype, B, H, n_q, n_kv, head_dim, mask, n_qb, n_kb, block_m, block_n,
+                         softmax_scale, is_causal, sink_size, window_size))
+    return rc;
+  GKI_REQUIRE(q && k && v && o && dout && lse && dq && dk && dv && delta, 1, "gki_bsa_bwd: null tensor");
+  GKI_REQUIRE(row_ptr && row_idx && col_ptr && col_idx && kv_order, 1, "gki_bsa_bwd: null schedule");
+  GKI_REQUIRE(n_qt == (n_q + kTileM - 1) / kTileM && n_kt == (n_kv + kTileN - 1) / kTileN, 1,
+              "gki_bsa_bwd: schedule shape mismatch");
+  GKI_REQUIRE(n_heavy >= 0 && n_heavy <= n_kt, 1, "gki_bsa_bwd: bad heavy-column count");
+  return bwd_dispatch(dtype, head_dim, g, q, k, v, o, dout, lse, dq, dk, dv, delta, row_ptr, row_idx,
+                      n_qt, col_ptr, col_idx, kv_order, n_heavy, n_kt, (hipStream_t)stream);
+}
+
+int64_t gki_bsa_decode_workspace_floats(int32_t B, int32_t H, int32_t n_q, int32_t head_dim,
+                                        int32_t n_splits) {
+  return (int64_t)B * H * n_splits * n_q * (head_dim + 2);
+}
+
+int gki_bsa_decode(const void* q, const void* k, const void* v, void* o, float* lse, int32_t dtype,
+                   int32_t B, int32_t H, int32_t n_q, int32_t n_kv, int32_t head_dim,
+                   const int32_t* tile_list, int32_t n_tiles, const int32_t* mask, int32_t n_qb,
+                   int32_t n_kb, int32_t block_m, int32_t block_n, float softmax_scale,
+                   int32_t is_causal, int32_t sink_size, int32_t window_size, float* workspace,
+                   int32_t n_splits, void* stream) {
+  Geom g;
+  if (int rc = make_geom(g, dtype, B, H, n_q, n_kv, head_dim, mask, n_qb, n_kb, block_m, block_n,
+                         softmax_scale, is_causal, sink_size, window_size))
+    return rc;
+  GKI_REQUIRE(q && k && v && o && lse && workspace, 1, "gki_bsa_decode: null pointer");
+  GKI_REQUIRE(n_q <= kDecodeMaxQ, 2, "gki_bsa_decode: n_q exceeds the decode kernel's row limit");
+  GKI_REQUIRE(n_tiles >= 0 && (n_tiles == 0 || tile_list), 1, "gki_bsa_decode: bad tile list");
+  GKI_REQUIRE(n_splits >= 1, 1, "gki_bsa_decode: n_splits must be >= 1");
+  GKI_REQUIRE((int64_t)n_tiles * kTileN <= (int64_t)n_splits * decode_max_tokens_per_split(), 1,
+              "gki_bsa_decode: too few splits for the kept-token count");
+  return decode_dispatch(dtype, head_dim, g, q, k, v, o, lse, tile_list, n_tiles, workspace, n_splits,
+                         (hipStream_t)stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,179 @@
+// Shared device/host helpers for the gfx950 block-sparse attention kernels.
+//
+// Everything here is CDNA4-specific: wave64, v_mfma_f32_16x16x32_{bf16,f16}
+// and v_mfma_f32_16x16x4f32 fragments, LDS staging helpers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+namespace gki {
+
+// ---------------------------------------------------------------------------
+// Element types. Storage is always the raw 16/32-bit pattern; conversions go
+// through __bf16 / _Float16 so the compiler emits v_cvt_pk_bf16_f32 (RNE) and
+// v_cvt_f16_f32 (RNE), matching torch's .to(dtype) rounding.
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+enum DType : int { kF32 = 0, kF16 = 1, kBF16 = 2 };
+
+struct F32 {
+  using storage = float;
+  static constexpr bool is_f32 = true;
+  __device__ static inline float to_float(float x) { return x; }
+  __device__ static inline float from_float(float x) { return x; }
+};
+struct F16 {
+  using storage = uint16_t;
+  using vec8 = f16x8;
+  static constexpr bool is_f32 = false;
+  __device__ static inline float to_float(uint16_t x) {
+    return (float)__builtin_bit_cast(_Float16, x);
+  }
+  __device__ static inline uint16_t from_float(float x) {
+    return __builtin_bit_cast(uint16_t, (_Float16)x);
+  }
+  __device__ static inline floatx4 mfma(const uint4& a, const uint4& b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+};
+struct BF16 {
+  using storage = uint16_t;
+  using vec8 = bf16x8;
+  static constexpr bool is_f32 = false;
+  __device__ static inline float to_float(uint16_t x) {
+    return __builtin_bit_cast(float, ((uint32_t)x) << 16);
+  }
+  __device__ static inline uint16_t from_float(float x) {
+    return __builtin_bit_cast(uint16_t, (__bf16)x);
+  }
+  __device__ static inline floatx4 mfma(const uint4& a, const uint4& b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+};
+
+__device__ inline floatx4 mfma_f32(float a, float b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// 16-byte streaming (non-temporal) global load.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+__device__ inline uint4 ld_nt16(const void* p) {
+  const u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// Pack 8 fp32 values into 8 16-bit elements (one 16x16x32 MFMA operand).
+template <typename T>
+__device__ inline uint4 pack8(const float* v) {
+  uint4 r;
+  r.x = (uint32_t)T::from_float(v[0]) | ((uint32_t)T::from_float(v[1]) << 16);
+  r.y = (uint32_t)T::from_float(v[2]) | ((uint32_t)T::from_float(v[3]) << 16);
+  r.z = (uint32_t)T::from_float(v[4]) | ((uint32_t)T::from_float(v[5]) << 16);
+  r.w = (uint32_t)T::from_float(v[6]) | ((uint32_t)T::from_float(v[7]) << 16);
+  return r;
+}
+
+// ---------------------------------------------------------------------------
+// Kernel tiling. All prefill / backward kernels use 64x64 (q x kv) tiles, four
+// waves per workgroup, each wave owning 16 rows of the tile's outer axis. The
+// decode kernel (n_q <= kDecodeMaxQ) uses a single 16-row q tile.
+// ---------------------------------------------------------------------------
+constexpr int kTileM = 64;
+constexpr int kTileN = 64;
+constexpr int kDecodeTileM = 16;
+constexpr int kDecodeMaxQ = 4;
+constexpr int kPartialBit = 30;       // schedule entry flag: needs per-element mask lookup
+constexpr int kIdxMask = (1 << kPartialBit) - 1;
+
+// Row permutation rho(t, j) of a 64-row tile into four 16-row MFMA subtiles.
+// Subtile t = 2s+h, lane-row j = 4a+i holds tile row 32s + 8a + 4h + i. With
+// this order the fp32 accumulator of subtiles (2s, 2s+1) held by lane group a
+// covers rows 32s+8a .. 32s+8a+7 contiguously, i.e. it already IS the 8-element
+// K-operand of a 16x16x32 MFMA over those rows: no register transpose needed.
+__device__ inline int rho(int t, int j) {
+  return ((t >> 1) << 5) + ((j >> 2) << 3) + ((t & 1) << 2) + (j & 3);
+}
+
+// Geometry + masking parameters shared by all attention kernels.
+struct Geom {
+  int B, H;
+  int n_q, n_kv, q_off;
+  float scale;        // natural-log softmax scale
+  float scale_log2;   // scale * log2(e)
+  int causal, sink, window;
+  // original block mask (used only for tiles flagged partial)
+  const int32_t* mask;
+  int n_qb, n_kb, bm, bn;
+};
+
+// StreamingLLM token predicate on absolute positions (k <= q) & (k < S | k >= q-W+1).
+__device__ inline bool token_visible(int q_abs, int k, int sink, int window) {
+  return (k <= q_abs) && (k < sink || k >= q_abs - window + 1);
+}
+
+// Full element predicate for (q row, kv column) of a tile flagged "needs mask".
+__device__ inline bool elem_valid(const Geom& g, int q_row, int kv, bool partial) {
+  if (q_row >= g.n_q || kv >= g.n_kv) return false;
+  if (g.causal && !token_visible(q_row + g.q_off, kv, g.sink, g.window)) return false;
+  if (partial && g.mask[(size_t)(q_row / g.bm) * g.n_kb + kv / g.bn] == 0) return false;
+  return true;
+}
+
+// True when every (q, kv) with q in [q_lo, q_hi], kv in [k_lo, k_hi] (inclusive,
+// already in bounds) is visible under the StreamingLLM token rule.
+__device__ inline bool tile_all_visible(const Geom& g, int q_lo, int q_hi, int k_lo, int k_hi) {
+  if (!g.causal) return true;
+  const int qa = q_lo + g.q_off, qb = q_hi + g.q_off;
+  if (k_hi > qa) return false;
+  return (k_hi < g.sink) || (k_lo >= qb - g.window + 1);
+}
+
+// XCD-aware remap: hardware dispatches workgroup b to XCD b % 8. Give each XCD
+// one contiguous range of logical ids so neighbouring q tiles of one head (which
+// share most K/V tiles) run on the same XCD and hit in its L2.
+__device__ inline int xcd_remap(int b, int n) {
+  constexpr int kXcd = 8;
+  const int xcd = b % kXcd, local = b / kXcd;
+  const int per = n / kXcd, rem = n % kXcd;
+  return (xcd < rem) ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+}
+
+__device__ inline float wave_max16x4(float x) {
+  // reduce across the 4 lane groups (lanes l, l^16, l^32, l^48)
+  x = fmaxf(x, __shfl_xor(x, 16));
+  x = fmaxf(x, __shfl_xor(x, 32));
+  return x;
+}
+__device__ inline float wave_sum16x4(float x) {
+  x += __shfl_xor(x, 16);
+  x += __shfl_xor(x, 32);
+  return x;
+}
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kNegInf = -__builtin_huge_valf();
+
+}  // namespace gki
+
+// ---------------------------------------------------------------------------
+// Host-side error plumbing for the C ABI.
+// ---------------------------------------------------------------------------
+namespace gki {
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+int check_launch(const char* what);
+}  // namespace gki
+
+#define GKI_REQUIRE(cond, code, msg)          \
+  do {                                        \
+    if (!(cond)) return ::gki::fail(code, msg); \
+  } while (0)

@@ -1,0 +1,176 @@
+"""GPU-resident kept-block lists and kernel schedules.
+
+The reference visits every ``(i, j)`` tile and skips it after a per-iteration
+int32 gate load (``sparse_triton_kernel.py:283-285, 448-450, 563-565``). Here the
+mask is turned once, on the GPU, into int32 lists:
+
+* ``build_block_lists(mask)`` -- CSR (row -> ascending kept columns) and CSC
+  (column -> ascending kept rows) of a 0/1 block mask. The CSR order is exactly
+  ``mask.nonzero()``.
+* ``prefill_schedule(...)`` -- the same lists over the kernels' fixed 64x64
+  tiles (a mask of any block size is first classified per tile by
+  ``gki_tile_mask``), plus the "heavy columns first" order for the dK/dV grid.
+* ``decode_schedule(...)`` -- the kept kv tiles of the single decode q tile.
+
+Schedules are cached per mask tensor (identity, version, geometry); the cache
+holds a reference to the mask so its storage cannot be recycled under the key.
+Building a schedule synchronises the stream once (to size the lists).
+"""
+
+from __future__ import annotations
+
+import threading
+from collections import OrderedDict
+from dataclasses import dataclass
+from typing import Tuple
+
+import torch
+
+from . import _lib
+
+
+@dataclass(frozen=True)
+class BlockLists:
+    """CSR + CSC kept-block lists of an int32 ``[n_rows, n_cols]`` matrix."""
+
+    row_ptr: torch.Tensor  # [n_rows + 1] int32
+    row_idx: torch.Tensor  # [nnz] int32, column | partial << 30
+    col_ptr: torch.Tensor  # [n_cols + 1] int32
+    col_idx: torch.Tensor  # [nnz] int32, row | partial << 30
+    n_rows: int
+    n_cols: int
+    nnz: int
+
+
+@dataclass(frozen=True)
+class PrefillSchedule:
+    lists: BlockLists         # over kernel tiles (n_qt x n_kt)
+    kv_order: torch.Tensor    # [n_kt] int32, heavy columns first
+    n_heavy: int
+    n_qt: int
+    n_kt: int
+
+
+@dataclass(frozen=True)
+class DecodeSchedule:
+    tiles: torch.Tensor       # [n_tiles] int32 kept kv tiles of q tile 0
+    n_tiles: int
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _lists_of(matrix: torch.Tensor) -> BlockLists:
+    """CSR/CSC of a {0,1,2}-valued int32 device matrix (2 marks partial)."""
+    lib = _lib.load()
+    n_rows, n_cols = (int(s) for s in matrix.shape)
+    dev = matrix.device
+    stream = _stream(dev)
+    row_cnt = torch.empty(n_rows, dtype=torch.int32, device=dev)
+    col_cnt = torch.empty(n_cols, dtype=torch.int32, device=dev)
+    row_ptr = torch.empty(n_rows + 1, dtype=torch.int32, device=dev)
+    col_ptr = torch.empty(n_cols + 1, dtype=torch.int32, device=dev)
+    _lib.check(lib.gki_block_list_counts(matrix.data_ptr(), n_rows, n_cols, row_cnt.data_ptr(),
+                                         col_cnt.data_ptr(), row_ptr.data_ptr(), col_ptr.data_ptr(),
+                                         stream), "gki_block_list_counts")
+    nnz = int(row_ptr[-1].item())  # one sync per (cached) schedule
+    row_idx = torch.empty(max(nnz, 1), dtype=torch.int32, device=dev)
+    col_idx = torch.empty(max(nnz, 1), dtype=torch.int32, device=dev)
+    _lib.check(lib.gki_block_list_fill(matrix.data_ptr(), n_rows, n_cols, row_ptr.data_ptr(),
+                                       col_ptr.data_ptr(), row_idx.data_ptr(), col_idx.data_ptr(),
+                                       stream), "gki_block_list_fill")
+    return BlockLists(row_ptr, row_idx[:nnz], col_ptr, col_idx[:nnz], n_rows, n_cols, nnz)
+
+
+def build_block_lists(block_mask: torch.Tensor) -> BlockLists:
+    """Kept-block lists of a block mask, computed by the gfx950 library.
+
+    ``block_mask`` must be a 2-D tensor on a GPU (any integer dtype; non-zero
+    means kept). ``row_idx`` equals ``block_mask.nonzero()[:, 1]`` and
+    ``col_idx`` equals ``block_mask.t().nonzero()[:, 1]``, bit for bit.
+    """
+    if block_mask.dim() != 2:
+        raise ValueError("block_mask must be 2-D")
+    if not block_mask.is_cuda:
+        raise ValueError("block_mask must live on a CUDA device")
+    m = (block_mask != 0).to(torch.int32).contiguous()
+    with torch.cuda.device(m.device):
+        return _lists_of(m)
+
+
+def _tile_matrix(mask: torch.Tensor, n_q: int, n_kv: int, block_m: int, block_n: int,
+                 tile_m: int, tile_n: int) -> torch.Tensor:
+    lib = _lib.load()
+    n_qb, n_kb = (int(s) for s in mask.shape)
+    n_qt, n_kt = -(-n_q // tile_m), -(-n_kv // tile_n)
+    out = torch.empty((n_qt, n_kt), dtype=torch.int32, device=mask.device)
+    _lib.check(lib.gki_tile_mask(mask.data_ptr(), n_qb, n_kb, block_m, block_n, n_q, n_kv, tile_m,
+                                 tile_n, out.data_ptr(), _stream(mask.device)), "gki_tile_mask")
+    return out
+
+
+class _ScheduleCache:
+    def __init__(self, capacity: int = 32) -> None:
+        self._d: "OrderedDict[tuple, Tuple[torch.Tensor, object]]" = OrderedDict()
+        self._cap = capacity
+        self._lock = threading.Lock()
+
+    def get(self, mask: torch.Tensor, key: tuple, build):
+        full = (mask.data_ptr(), mask._version, tuple(mask.shape), str(mask.device)) + key
+        with self._lock:
+            hit = self._d.get(full)
+            if hit is not None and hit[0] is mask:
+                self._d.move_to_end(full)
+                return hit[1]
+        value = build()
+        with self._lock:
+            self._d[full] = (mask, value)
+            self._d.move_to_end(full)
+            while len(self._d) > self._cap:
+                self._d.popitem(last=False)
+        return value
+
+    def clear(self) -> None:
+        with self._lock:
+            self._d.clear()
+
+
+_CACHE = _ScheduleCache()
+
+
+def clear_schedule_cache() -> None:
+    _CACHE.clear()
+
+
+def prefill_schedule(mask: torch.Tensor, n_q: int, n_kv: int, block_m: int,
+                     block_n: int) -> PrefillSchedule:
+    """Schedules for the prefill forward, dQ and dK/dV kernels (64x64 tiles)."""
+    ts = _lib.tile_sizes()
+    tm, tn = ts["tile_m"], ts["tile_n"]
+
+    def build() -> PrefillSchedule:
+        lib = _lib.load()
+        tiles = _tile_matrix(mask, n_q, n_kv, block_m, block_n, tm, tn)
+        lists = _lists_of(tiles)
+        order = torch.empty(lists.n_cols, dtype=torch.int32, device=mask.device)
+        n_heavy = torch.empty(1, dtype=torch.int32, device=mask.device)
+        _lib.check(lib.gki_heavy_order(lists.col_ptr.data_ptr(), lists.n_cols, order.data_ptr(),
+                                       n_heavy.data_ptr(), _stream(mask.device)), "gki_heavy_order")
+        return PrefillSchedule(lists, order, int(n_heavy.item()), lists.n_rows, lists.n_cols)
+
+    return _CACHE.get(mask, ("prefill", n_q, n_kv, block_m, block_n, tm, tn), build)
+
+
+def decode_schedule(mask: torch.Tensor, n_q: int, n_kv: int, block_m: int,
+                    block_n: int) -> DecodeSchedule:
+    """Kept kv tiles (64 keys each) of the single decode q tile (n_q rows)."""
+    ts = _lib.tile_sizes()
+    tm, tn = ts["decode_tile_m"], ts["tile_n"]
+
+    def build() -> DecodeSchedule:
+        tiles = _tile_matrix(mask, n_q, n_kv, block_m, block_n, tm, tn)
+        lists = _lists_of(tiles)
+        return DecodeSchedule(lists.row_idx, lists.nnz)
+
+    return _CACHE.get(mask, ("decode", n_q, n_kv, block_m, block_n, tm, tn), build)

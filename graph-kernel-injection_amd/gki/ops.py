@@ -1,0 +1,194 @@
+"""Autograd bridge and public op: block-sparse FlashAttention on gfx950.
+
+Drop-in for the reference's ``_BlockSparseFlashAttention`` and
+``block_sparse_attention`` (``sparse_triton_kernel.py:609-837``): same
+signatures, same validation order, exception types and messages, same saved
+state and gradient tuple. The Triton launches are replaced by calls into the
+C ABI of ``libgki_bsa.so`` on the caller's current HIP stream:
+
+* forward  -> ``gki_bsa_fwd`` (prefill) or ``gki_bsa_decode`` (n_q <= 4,
+  head_dim 64/128: the decode step),
+* backward -> ``gki_bsa_bwd`` (Delta, dK/dV, dQ).
+
+There is no CPU or eager fallback: a missing library raises ``RuntimeError``.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+from .lists import _CACHE, decode_schedule, prefill_schedule
+
+_DTYPE_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+_HEAD_DIMS = (16, 32, 64, 128)
+_DECODE_HEAD_DIMS = (64, 128)
+# total decode workgroups to aim for (256 CUs x 16 resident 256-thread groups)
+_DECODE_TARGET_WGS = 4096
+
+
+def _device_mask(block_mask: torch.Tensor, device: torch.device) -> torch.Tensor:
+    """int32 contiguous copy of the mask on ``device`` (cached for CPU masks)."""
+    if block_mask.device == device and block_mask.dtype == torch.int32 and block_mask.is_contiguous():
+        return block_mask
+    if block_mask.device.type == "cpu":
+        return _CACHE.get(block_mask, ("device-copy", str(device)),
+                          lambda: block_mask.to(device=device, dtype=torch.int32).contiguous())
+    return block_mask.to(device=device, dtype=torch.int32).contiguous()
+
+
+def _decode_splits(n_tiles: int, bh: int, tile_n: int, max_tokens: int) -> int:
+    est = max(n_tiles, 1) * tile_n
+    need = -(-est // max_tokens)              # at most max_tokens tokens per split
+    want = -(-_DECODE_TARGET_WGS // bh)       # fill the machine
+    cap = max(1, est // tile_n)               # at least one tile of tokens per split
+    return max(need, min(want, cap))
+
+
+class _BlockSparseFlashAttention(torch.autograd.Function):
+    """Autograd bridge between PyTorch and the gfx950 kernels."""
+
+    @staticmethod
+    def forward(  # type: ignore[override]
+        ctx,
+        q: torch.Tensor,
+        k: torch.Tensor,
+        v: torch.Tensor,
+        block_mask: torch.Tensor,
+        softmax_scale: float,
+        block_m: int,
+        block_n: int,
+        is_causal: bool,
+        sink_size: int,
+        window_size: int,
+    ) -> torch.Tensor:
+        lib = _lib.load()
+        if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+            raise ValueError("Q/K/V must be 4-D [B, H, N, D] tensors")
+        if not (q.is_cuda and k.is_cuda and v.is_cuda):
+            raise ValueError("All inputs must live on a CUDA device")
+
+        B, H, N_Q, D = q.shape
+        N_KV = k.shape[2]
+        if k.shape != v.shape:
+            raise ValueError("K and V must share shape")
+        if k.shape[:2] != q.shape[:2] or k.shape[-1] != D:
+            raise ValueError("Q/K/V batch/head/dim mismatch")
+        if not (q.dtype == k.dtype == v.dtype) or q.dtype not in _DTYPE_CODE:
+            raise ValueError(
+                f"Q/K/V must share one dtype among float32/float16/bfloat16, got "
+                f"{q.dtype}/{k.dtype}/{v.dtype}")
+        if D not in _HEAD_DIMS:
+            raise ValueError(f"head_dim must be one of {_HEAD_DIMS}, got {D}")
+
+        block_m, block_n = int(block_m), int(block_n)
+        n_qb = (N_Q + block_m - 1) // block_m
+        n_kb = (N_KV + block_n - 1) // block_n
+        if block_mask.shape != (n_qb, n_kb):
+            raise ValueError(
+                f"block_mask has shape {tuple(block_mask.shape)}, "
+                f"expected {(n_qb, n_kb)}"
+            )
+        q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+        dev = q.device
+        block_mask = _device_mask(block_mask, dev)
+
+        o = torch.empty_like(q)
+        lse = torch.empty((B, H, N_Q), dtype=torch.float32, device=dev)
+        q_offset = N_KV - N_Q
+        dtype = _DTYPE_CODE[q.dtype]
+        common = (block_mask.data_ptr(), n_qb, n_kb, block_m, block_n, float(softmax_scale),
+                  int(bool(is_causal)), int(sink_size), int(window_size))
+
+        with torch.cuda.device(dev):
+            stream = torch.cuda.current_stream(dev).cuda_stream
+            ts = _lib.tile_sizes()
+            if N_Q <= ts["decode_max_q"] and D in _DECODE_HEAD_DIMS:
+                sched = decode_schedule(block_mask, N_Q, N_KV, block_m, block_n)
+                n_splits = _decode_splits(sched.n_tiles, B * H, ts["tile_n"], ts["decode_max_tokens"])
+                ws = torch.empty(int(lib.gki_bsa_decode_workspace_floats(B, H, N_Q, D, n_splits)),
+                                 dtype=torch.float32, device=dev)
+                _lib.check(lib.gki_bsa_decode(
+                    q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), dtype,
+                    B, H, N_Q, N_KV, D, sched.tiles.data_ptr(), sched.n_tiles, *common,
+                    ws.data_ptr(), n_splits, stream), "gki_bsa_decode")
+            else:
+                sched = prefill_schedule(block_mask, N_Q, N_KV, block_m, block_n)
+                _lib.check(lib.gki_bsa_fwd(
+                    q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), dtype,
+                    B, H, N_Q, N_KV, D, sched.lists.row_ptr.data_ptr(),
+                    sched.lists.row_idx.data_ptr(), sched.n_qt, *common, stream), "gki_bsa_fwd")
+
+        ctx.save_for_backward(q, k, v, o, lse, block_mask)
+        ctx.softmax_scale = softmax_scale
+        ctx.block_m = block_m
+        ctx.block_n = block_n
+        ctx.is_causal = bool(is_causal)
+        ctx.sink_size = int(sink_size)
+        ctx.window_size = int(window_size)
+        ctx.q_offset = int(q_offset)
+        return o
+
+    @staticmethod
+    def backward(  # type: ignore[override]
+        ctx, do: torch.Tensor
+    ) -> Tuple[Optional[torch.Tensor], ...]:
+        lib = _lib.load()
+        q, k, v, o, lse, block_mask = ctx.saved_tensors
+        do = do.to(q.dtype).contiguous()
+        B, H, N_Q, D = q.shape
+        N_KV = k.shape[2]
+        n_qb = (N_Q + ctx.block_m - 1) // ctx.block_m
+        n_kb = (N_KV + ctx.block_n - 1) // ctx.block_n
+
+        dq = torch.empty_like(q)
+        dk = torch.empty_like(k)
+        dv = torch.empty_like(v)
+        delta = torch.empty((B, H, N_Q), dtype=torch.float32, device=q.device)
+        with torch.cuda.device(q.device):
+            stream = torch.cuda.current_stream(q.device).cuda_stream
+            sched = prefill_schedule(block_mask, N_Q, N_KV, ctx.block_m, ctx.block_n)
+            L = sched.lists
+            _lib.check(lib.gki_bsa_bwd(
+                q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(),
+                lse.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), delta.data_ptr(),
+                _DTYPE_CODE[q.dtype], B, H, N_Q, N_KV, D, L.row_ptr.data_ptr(),
+                L.row_idx.data_ptr(), sched.n_qt, L.col_ptr.data_ptr(), L.col_idx.data_ptr(),
+                sched.kv_order.data_ptr(), sched.n_heavy, sched.n_kt, block_mask.data_ptr(), n_qb,
+                n_kb, ctx.block_m, ctx.block_n, float(ctx.softmax_scale), int(ctx.is_causal),
+                ctx.sink_size, ctx.window_size, stream), "gki_bsa_bwd")
+        return dq, dk, dv, None, None, None, None, None, None, None
+
+
+def block_sparse_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    block_mask: torch.Tensor,
+    softmax_scale: Optional[float] = None,
+    block_m: int = 64,
+    block_n: int = 64,
+    is_causal: bool = False,
+    sink_size: int = 0,
+    window_size: int = 0,
+) -> torch.Tensor:
+    """Differentiable block-sparse FlashAttention (``sparse_triton_kernel.py:787-837``).
+
+    ``q, k, v``: ``[B, H, N, D]`` on the GPU, one dtype among fp32/fp16/bf16,
+    ``D`` in {16, 32, 64, 128}. ``block_mask``: ``[ceil(N_Q/block_m),
+    ceil(N_KV/block_n)]``, non-zero = visit. With ``is_causal=True`` every
+    visited tile also applies the token rule
+    ``(k <= q) & (k < sink_size | k >= q - window_size + 1)`` with queries
+    bottom-right aligned (``q = N_KV - N_Q + row``). ``softmax_scale`` defaults
+    to ``1/sqrt(D)``. Rows that see no key produce zeros (and zero gradients).
+    """
+    if softmax_scale is None:
+        softmax_scale = 1.0 / math.sqrt(q.shape[-1])
+    return _BlockSparseFlashAttention.apply(
+        q.contiguous(), k.contiguous(), v.contiguous(),
+        block_mask, float(softmax_scale), int(block_m), int(block_n),
+        bool(is_causal), int(sink_size), int(window_size),
+    )

@@ -1,0 +1,129 @@
+/*
+ * gki_bsa.h -- C ABI of the MI355X (gfx950) block-sparse StreamingLLM
+ * FlashAttention library `libgki_bsa.so`.
+ *
+ * Conventions
+ *  - Tensors are device pointers to contiguous [B, H, N, D] arrays (BHND,
+ *    row-major), as produced by `.contiguous()` in the reference
+ *    (sparse_triton_kernel.py:834). LSE / Delta are contiguous fp32 [B, H, N_Q].
+ *  - dtype codes: 0 = fp32, 1 = fp16, 2 = bf16. head_dim in {16, 32, 64, 128}.
+ *  - The block mask is an int32 [n_qb, n_kb] device array with
+ *    n_qb = ceil(N_Q / block_m), n_kb = ceil(N_KV / block_n), shared across B, H.
+ *  - Kernel schedules are int32 CSR / CSC lists over the kernels' fixed tiles
+ *    (see gki_tile_sizes); entries are `tile_index | partial << 30`, where
+ *    `partial` marks a tile only partly covered by kept mask blocks.
+ *  - `stream` is a hipStream_t. Every call is asynchronous on it, never
+ *    allocates or frees device memory, and keeps no pointer after returning.
+ *  - Return value: 0 on success; otherwise non-zero (1 = bad argument,
+ *    2 = unsupported configuration, 3 = HIP launch error), with the message in
+ *    gki_last_error() (thread-local).
+ */
+#ifndef GKI_BSA_H_
+#define GKI_BSA_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ABI version (currently 1). */
+int gki_abi_version(void);
+
+/* Message of the last failing call on this thread. */
+const char* gki_last_error(void);
+
+/* Kernel tile geometry the schedules must be built for: prefill/backward tile
+ * (tile_m x tile_n), decode q tile rows, max query rows handled by the decode
+ * kernel, and max tokens one decode split holds. Any pointer may be NULL. */
+int gki_tile_sizes(int32_t* tile_m, int32_t* tile_n, int32_t* decode_tile_m,
+                   int32_t* decode_max_q, int32_t* decode_max_tokens);
+
+/* Block-level StreamingLLM mask, bit-exact with `make_streaming_mask`
+ * (sparse_triton_kernel.py:104-181): keep (i, j) iff q_hi > k_lo and
+ * (k_lo < sink or k_hi - 1 >= q_lo - window + 1), q_lo = i*block_m + n_kv - n_q.
+ * `mask` holds ceil(n_q/block_m) * ceil(n_kv/block_n) int32. */
+int gki_streaming_mask(int32_t* mask, int64_t n_q, int64_t n_kv, int64_t sink,
+                       int64_t window, int64_t block_m, int64_t block_n, void* stream);
+
+/* Dense / dense-causal block mask, `make_dense_mask`
+ * (sparse_triton_kernel.py:184-210); requires block sizes dividing n_q, n_kv. */
+int gki_dense_mask(int32_t* mask, int64_t n_q, int64_t n_kv, int64_t block_m,
+                   int64_t block_n, int32_t causal, void* stream);
+
+/* Classify the kernels' tile_m x tile_n tiles against a block mask of any
+ * granularity: 0 = no kept block overlaps, 1 = all overlapping blocks kept,
+ * 2 = partly kept. No reference counterpart: the reference gates its Triton
+ * tiles directly on the mask (sparse_triton_kernel.py:283-285). */
+int gki_tile_mask(const int32_t* mask, int32_t n_qb, int32_t n_kb, int32_t block_m,
+                  int32_t block_n, int32_t n_q, int32_t n_kv, int32_t tile_m,
+                  int32_t tile_n, int32_t* tile_mask, void* stream);
+
+/* Kept-block list, step 1: per-row / per-column kept counts of an int32
+ * [n_rows, n_cols] matrix and their exclusive prefix sums (row_ptr[n_rows+1],
+ * col_ptr[n_cols+1]). Replaces the reference's per-iteration int32 gate loads
+ * (sparse_triton_kernel.py:283-285, 448-450, 563-565) with a CSR/CSC list. */
+int gki_block_list_counts(const int32_t* m, int32_t n_rows, int32_t n_cols,
+                          int32_t* row_cnt, int32_t* col_cnt, int32_t* row_ptr,
+                          int32_t* col_ptr, void* stream);
+
+/* Kept-block list, step 2: fill CSR (row -> ascending columns) and/or CSC
+ * (column -> ascending rows) indices; either output may be NULL. For a 0/1
+ * mask the CSR order equals `mask.nonzero()`. */
+int gki_block_list_fill(const int32_t* m, int32_t n_rows, int32_t n_cols,
+                        const int32_t* row_ptr, const int32_t* col_ptr,
+                        int32_t* row_idx, int32_t* col_idx, void* stream);
+
+/* Column order for the dK/dV grid: columns kept by more than twice the mean
+ * row count (the StreamingLLM sink column) first, then the rest, each group
+ * ascending. Writes n_cols indices and the heavy count (device scalar). */
+int gki_heavy_order(const int32_t* col_ptr, int32_t n_cols, int32_t* order,
+                    int32_t* n_heavy, void* stream);
+
+/* Prefill forward: replaces the `_fwd_kernel` launch in
+ * `_BlockSparseFlashAttention.forward` (sparse_triton_kernel.py:662-682).
+ * O = softmax(mask(Q K^T * scale)) V, LSE = m + ln(l) (0 for empty rows).
+ * row_ptr/row_idx: CSR over ceil(n_q/tile_m) q tiles of kept kv tiles. */
+int gki_bsa_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
+                int32_t dtype, int32_t B, int32_t H, int32_t n_q, int32_t n_kv,
+                int32_t head_dim, const int32_t* row_ptr, const int32_t* row_idx,
+                int32_t n_qt, const int32_t* mask, int32_t n_qb, int32_t n_kb,
+                int32_t block_m, int32_t block_n, float softmax_scale, int32_t is_causal,
+                int32_t sink_size, int32_t window_size, void* stream);
+
+/* Backward: replaces the three launches in `_BlockSparseFlashAttention.backward`
+ * (sparse_triton_kernel.py:719-777): Delta = rowsum(O * dO) into `delta`, then
+ * dK/dV over the CSC list (kv_order / n_heavy from gki_heavy_order), then dQ
+ * over the CSR list. dq, dk, dv are fully written (no zero-fill needed). */
+int gki_bsa_bwd(const void* q, const void* k, const void* v, const void* o,
+                const void* dout, const float* lse, void* dq, void* dk, void* dv,
+                float* delta, int32_t dtype, int32_t B, int32_t H, int32_t n_q,
+                int32_t n_kv, int32_t head_dim, const int32_t* row_ptr,
+                const int32_t* row_idx, int32_t n_qt, const int32_t* col_ptr,
+                const int32_t* col_idx, const int32_t* kv_order, int32_t n_heavy,
+                int32_t n_kt, const int32_t* mask, int32_t n_qb, int32_t n_kb,
+                int32_t block_m, int32_t block_n, float softmax_scale, int32_t is_causal,
+                int32_t sink_size, int32_t window_size, void* stream);
+
+/* Floats of workspace gki_bsa_decode needs for a given split count. */
+int64_t gki_bsa_decode_workspace_floats(int32_t B, int32_t H, int32_t n_q,
+                                        int32_t head_dim, int32_t n_splits);
+
+/* Decode step (n_q <= decode_max_q, head_dim 64 or 128): replaces the
+ * reference's BLOCK_M = 1 use of `_fwd_kernel` for decode
+ * (benchmark.py:500-511, 802-804) with a split-KV pass over the kept kv tiles
+ * of the single decode q tile (`tile_list`, n_tiles entries) and a combine.
+ * Same outputs as gki_bsa_fwd. n_tiles * tile_n <= n_splits * decode_max_tokens. */
+int gki_bsa_decode(const void* q, const void* k, const void* v, void* o, float* lse,
+                   int32_t dtype, int32_t B, int32_t H, int32_t n_q, int32_t n_kv,
+                   int32_t head_dim, const int32_t* tile_list, int32_t n_tiles,
+                   const int32_t* mask, int32_t n_qb, int32_t n_kb, int32_t block_m,
+                   int32_t block_n, float softmax_scale, int32_t is_causal,
+                   int32_t sink_size, int32_t window_size, float* workspace,
+                   int32_t n_splits, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GKI_BSA_H_ */

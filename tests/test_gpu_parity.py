@@ -1,0 +1,336 @@
+"""GPU parity of the gfx950 kernels against the oracle.
+
+* masks and kept-block lists: bit-exact against ``oracle.streaming_oracle``;
+* forward / backward / decode: against the fp64 oracle on small shapes and
+  against the chunked exact reference (``oracle.chunked_reference``, fp64 on
+  the GPU) at the full sizes of the five BASELINE configs.
+
+Tolerances: fp32 atol 1e-5; fp16/bf16 atol 2e-2 and
+rtol 1e-2, i.e. |ours - ref| <= atol + rtol * |ref| elementwise.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import fx_compiler_pass as fxp
+import sparse_triton_kernel as stk
+from gki import build_block_lists
+from gki.lists import decode_schedule, prefill_schedule
+from oracle import chunked_reference as cr
+from oracle import streaming_oracle as so
+
+from test_oracle_pins import BLOCK_SHAPES
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TOL = {torch.float32: (1e-5, 0.0), torch.float16: (2e-2, 1e-2), torch.bfloat16: (2e-2, 1e-2)}
+
+
+def _close(ours: torch.Tensor, ref: torch.Tensor, dtype: torch.dtype, what: str) -> None:
+    atol, rtol = TOL[dtype]
+    o = ours.detach().to(torch.float64).cpu()
+    r = ref.detach().to(torch.float64).cpu()
+    err = (o - r).abs()
+    bound = atol + rtol * r.abs()
+    bad = err > bound
+    assert torch.isfinite(o).all(), f"{what}: non-finite values"
+    assert not bad.any(), (f"{what}: {int(bad.sum())} elements out of tolerance, max|d|="
+                           f"{float(err.max()):.3e}, worst excess={float((err - bound).max()):.3e}")
+
+
+def _inputs(shape_q, shape_kv, dtype, seed, scale=1.0, device_gen=False, grad_out=False):
+    if device_gen:
+        g = torch.Generator(device=DEV).manual_seed(seed)
+        mk = lambda s: (torch.randn(s, generator=g, device=DEV, dtype=torch.float32) * scale).to(dtype)
+    else:
+        g = torch.Generator().manual_seed(seed)
+        mk = lambda s: (torch.randn(s, generator=g, dtype=torch.float32) * scale).to(dtype).to(DEV)
+    q, k, v = mk(shape_q), mk(shape_kv), mk(shape_kv)
+    do = mk(shape_q) if grad_out else None
+    return q, k, v, do
+
+
+# ---------------------------------------------------------------------------
+# masks and lists: bit-exact
+# ---------------------------------------------------------------------------
+
+CONFIG_MASKS = [
+    (1024, 1024, 4, 256, 64, 64), (16384, 16384, 4, 2048, 64, 64), (8192, 8192, 4, 1024, 64, 64),
+    (1, 100000, 4, 2048, 1, 64), (131072, 131072, 4, 4096, 128, 64),
+]
+
+
+@pytest.mark.parametrize("n_q,n_kv,sink,window,bm,bn", BLOCK_SHAPES + CONFIG_MASKS)
+def test_device_streaming_mask_bit_exact(n_q, n_kv, sink, window, bm, bn):
+    m = stk.make_streaming_mask(n_q, n_kv, stk.StreamingMaskSpec(sink, window), bm, bn, device=DEV)
+    assert m.dtype == torch.int32 and m.is_cuda
+    np.testing.assert_array_equal(m.cpu().numpy(), so.block_mask(n_q, n_kv, sink, window, bm, bn))
+
+
+def test_device_dense_mask_bit_exact():
+    for causal in (False, True):
+        m = stk.make_dense_mask(256, 512, 32, 64, causal=causal, device=DEV)
+        np.testing.assert_array_equal(m.cpu().numpy(), so.dense_block_mask(256, 512, 32, 64, causal))
+
+
+@pytest.mark.parametrize("n_q,n_kv,sink,window,bm,bn", CONFIG_MASKS + [(1000, 1000, 4, 128, 64, 64)])
+def test_kept_block_lists_bit_exact(n_q, n_kv, sink, window, bm, bn):
+    m = so.block_mask(n_q, n_kv, sink, window, bm, bn)
+    lists = build_block_lists(torch.from_numpy(m).to(DEV))
+    ref = so.kept_lists(m)
+    for got, want in zip((lists.row_ptr, lists.row_idx, lists.col_ptr, lists.col_idx), ref):
+        np.testing.assert_array_equal(got.cpu().numpy(), want)
+    assert lists.nnz == int(m.sum())
+
+
+def test_kept_block_lists_random_and_empty():
+    rng = np.random.default_rng(5)
+    for shape, p in (((37, 1500), 0.2), ((1, 1), 1.0), ((5, 7), 0.0), ((300, 2), 0.5)):
+        m = (rng.random(shape) < p).astype(np.int32)
+        lists = build_block_lists(torch.from_numpy(m).to(DEV))
+        for got, want in zip((lists.row_ptr, lists.row_idx, lists.col_ptr, lists.col_idx),
+                             so.kept_lists(m)):
+            np.testing.assert_array_equal(got.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("n_q,n_kv,sink,window,bm,bn",
+                         [(300, 300, 4, 64, 16, 16), (1000, 1000, 4, 128, 128, 32),
+                          (8192, 8192, 4, 1024, 64, 64), (200, 333, 2, 50, 8, 128)])
+def test_prefill_schedule_matches_oracle(n_q, n_kv, sink, window, bm, bn):
+    m = so.block_mask(n_q, n_kv, sink, window, bm, bn)
+    sched = prefill_schedule(torch.from_numpy(m).to(DEV), n_q, n_kv, bm, bn)
+    tiles = so.tile_classes(m, n_q, n_kv, bm, bn, 64, 64)
+    ref = so.kept_lists(tiles)
+    L = sched.lists
+    for got, want in zip((L.row_ptr, L.row_idx, L.col_ptr, L.col_idx), ref):
+        np.testing.assert_array_equal(got.cpu().numpy(), want)
+    order, n_heavy = so.heavy_order(ref[2])
+    np.testing.assert_array_equal(sched.kv_order.cpu().numpy(), order)
+    assert sched.n_heavy == n_heavy
+
+
+def test_decode_schedule_matches_oracle():
+    m = so.block_mask(1, 100000, 4, 2048, 1, 64)
+    sched = decode_schedule(torch.from_numpy(m).to(DEV), 1, 100000, 1, 64)
+    assert sched.n_tiles == 34
+    np.testing.assert_array_equal(sched.tiles.cpu().numpy(), [0] + list(range(1530, 1563)))
+
+
+# ---------------------------------------------------------------------------
+# small shapes vs the fp64 oracle
+# ---------------------------------------------------------------------------
+
+
+def _oracle(q, k, v, mask, bm, bn, causal, sink, window, scale, do=None):
+    n_q, n_kv = q.shape[-2], k.shape[-2]
+    eff = so.effective_mask(mask.cpu().numpy(), n_q, n_kv, bm, bn, causal, sink, window)
+    qn, kn, vn = (t.detach().to(torch.float64).cpu().numpy() for t in (q, k, v))
+    o, lse = so.attention_fwd(qn, kn, vn, eff, scale)
+    grads = None
+    if do is not None:
+        grads = so.attention_bwd(qn, kn, vn, do.detach().to(torch.float64).cpu().numpy(), eff, scale)
+    return torch.from_numpy(o), torch.from_numpy(lse), grads
+
+
+def _run_case(B, H, n_q, n_kv, D, dtype, bm, bn, causal, sink, window, seed, mask=None,
+              backward=True):
+    q, k, v, do = _inputs((B, H, n_q, D), (B, H, n_kv, D), dtype, seed, grad_out=True)
+    if mask is None:
+        mask = stk.make_streaming_mask(n_q, n_kv, stk.StreamingMaskSpec(sink, window), bm, bn, device=DEV)
+    scale = 1.0 / math.sqrt(D)
+    leaves = [t.clone().requires_grad_(backward) for t in (q, k, v)]
+    out = stk.block_sparse_attention(*leaves, mask, block_m=bm, block_n=bn, is_causal=causal,
+                                     sink_size=sink, window_size=window)
+    o_ref, lse_ref, grads = _oracle(q, k, v, mask, bm, bn, causal, sink, window, scale,
+                                    do if backward else None)
+    tag = f"B{B} H{H} nq{n_q} nkv{n_kv} D{D} {dtype} bm{bm} bn{bn} causal{causal} S{sink} W{window}"
+    _close(out, o_ref, dtype, "O " + tag)
+    if backward:
+        out.backward(do)
+        for name, t, ref in zip(("dQ", "dK", "dV"), leaves, grads):
+            _close(t.grad, torch.from_numpy(ref), dtype, f"{name} {tag}")
+    return out
+
+
+SMALL = [
+    # (B, H, n_q, n_kv, D, bm, bn, S, W)
+    (1, 2, 64, 64, 64, 64, 64, 4, 16),
+    (1, 2, 200, 200, 64, 64, 64, 4, 50),
+    (2, 1, 130, 333, 32, 64, 64, 3, 90),
+    (1, 2, 1000, 1000, 128, 64, 64, 4, 128),
+    (1, 1, 1025, 1025, 64, 64, 64, 4, 128),
+    (1, 2, 1023, 1023, 16, 64, 64, 4, 128),
+    (1, 2, 256, 256, 64, 128, 64, 4, 64),
+    (1, 2, 300, 300, 64, 16, 16, 4, 64),
+    (1, 1, 257, 700, 128, 32, 128, 2, 100),
+    (1, 2, 48, 1000, 64, 16, 64, 4, 128),
+    (1, 2, 128, 128, 64, 64, 64, 0, 64),
+    (1, 2, 128, 128, 64, 64, 64, 4, 0),
+    (1, 2, 64, 64, 64, 16, 16, 64, 0),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("case", SMALL, ids=lambda c: "x".join(map(str, c)))
+def test_small_causal_vs_oracle(case, dtype):
+    B, H, n_q, n_kv, D, bm, bn, S, W = case
+    _run_case(B, H, n_q, n_kv, D, dtype, bm, bn, True, S, W, seed=hash(case) % 1000)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("n_q,n_kv,D,bm,bn", [(1, 700, 64, 1, 64), (1, 1000, 128, 1, 64),
+                                               (3, 500, 128, 1, 64), (4, 129, 64, 2, 32),
+                                               (1, 64, 128, 1, 64), (2, 2000, 64, 1, 16)])
+def test_decode_vs_oracle(n_q, n_kv, D, bm, bn, dtype):
+    _run_case(2, 3, n_q, n_kv, D, dtype, bm, bn, True, 4, 256, seed=n_kv + D, backward=dtype == torch.float32)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_custom_noncausal_mask_vs_oracle(dtype):
+    rng = np.random.default_rng(11)
+    n_q, n_kv, bm, bn = 200, 260, 32, 16
+    m = (rng.random((-(-n_q // bm), -(-n_kv // bn))) < 0.35).astype(np.int32)
+    m[2] = 0                                            # rows 64..95 see nothing
+    _run_case(1, 2, n_q, n_kv, 64, dtype, bm, bn, False, 0, 0, seed=3,
+              mask=torch.from_numpy(m).to(DEV))
+
+
+def test_fully_masked_row_outputs_zero_and_no_nan():
+    """The reference's GPU test (tests/test_fully_masked_row.py:28-69)."""
+    B, H, N_Q, N_KV, D, bm = 1, 2, 32, 32, 16, 16
+    q, k, v = (torch.randn(B, H, n, D, device=DEV, requires_grad=True) for n in (N_Q, N_KV, N_KV))
+    mask = torch.zeros((2, 2), dtype=torch.int32, device=DEV)
+    mask[1, 1] = 1
+    out = stk.block_sparse_attention(q, k, v, mask, block_m=bm, block_n=bm, is_causal=False)
+    assert torch.isfinite(out).all()
+    assert torch.equal(out[:, :, :bm], torch.zeros_like(out[:, :, :bm]))
+    out.backward(torch.randn_like(out))
+    for g in (q.grad, k.grad, v.grad):
+        assert g is not None and torch.isfinite(g).all()
+    assert torch.equal(q.grad[:, :, :bm], torch.zeros_like(q.grad[:, :, :bm]))
+    assert torch.equal(k.grad[:, :, :bm], torch.zeros_like(k.grad[:, :, :bm]))
+
+
+def test_decode_and_prefill_paths_agree():
+    """n_q <= 4 goes through the split-KV decode kernel; n_q = 5 through prefill."""
+    B, H, n_kv, D = 2, 4, 3000, 128
+    k = torch.randn(B, H, n_kv, D, device=DEV, dtype=torch.bfloat16)
+    v = torch.randn(B, H, n_kv, D, device=DEV, dtype=torch.bfloat16)
+    q5 = torch.randn(B, H, 5, D, device=DEV, dtype=torch.bfloat16)
+    spec = stk.StreamingMaskSpec(4, 512)
+    o5 = stk.block_sparse_attention(q5, k, v, stk.make_streaming_mask(5, n_kv, spec, 1, 64, DEV),
+                                    block_m=1, block_n=64, is_causal=True, sink_size=4, window_size=512)
+    o4 = stk.block_sparse_attention(q5[:, :, 1:].contiguous(), k, v,
+                                    stk.make_streaming_mask(4, n_kv, spec, 1, 64, DEV),
+                                    block_m=1, block_n=64, is_causal=True, sink_size=4, window_size=512)
+    _close(o4, o5[:, :, 1:].float(), torch.bfloat16, "decode vs prefill")
+
+
+# ---------------------------------------------------------------------------
+# config 1: FX-rewritten StandardAttention, fp32 fwd + bwd
+# ---------------------------------------------------------------------------
+
+
+def test_config1_fx_rewrite_fp32_fwd_bwd():
+    B, H, N, D, S, W = 1, 4, 1024, 64, 4, 256
+    g = torch.Generator().manual_seed(0)
+    q, k, v = (torch.randn(B, H, N, D, generator=g) for _ in range(3))
+    cfg = fxp.InjectionConfig(seq_len_q=N, seq_len_kv=N, head_dim=D,
+                              streaming=stk.StreamingMaskSpec(S, W), block_m=64, block_n=64)
+    fused = fxp.BlockSparseAttentionInjector(cfg).transform(fxp.StandardAttention(D)).to(DEV)
+    leaves = [t.to(DEV).requires_grad_(True) for t in (q, k, v)]
+    out = fused(*leaves)
+    do = torch.randn(out.shape, generator=torch.Generator().manual_seed(1)).to(DEV)
+    out.backward(do)
+    mask = so.block_mask(N, N, S, W, 64, 64)
+    eff = so.effective_mask(mask, N, N, 64, 64, True, S, W)
+    qn, kn, vn, dn = (t.double().numpy() for t in (q, k, v, do.cpu()))
+    o_ref, _ = so.attention_fwd(qn, kn, vn, eff, 1 / 8)
+    grads = so.attention_bwd(qn, kn, vn, dn, eff, 1 / 8)
+    _close(out, torch.from_numpy(o_ref), torch.float32, "c1 O")
+    for name, t, ref in zip(("dQ", "dK", "dV"), leaves, grads):
+        _close(t.grad, torch.from_numpy(ref), torch.float32, f"c1 {name}")
+
+
+# ---------------------------------------------------------------------------
+# full-size configs vs the chunked exact reference (fp64 on the GPU)
+# ---------------------------------------------------------------------------
+
+
+def test_config2_prefill_bf16_full():
+    B, H, N, D, S, W, bm = 1, 32, 16384, 128, 4, 2048, 64
+    q, k, v, _ = _inputs((B, H, N, D), (B, H, N, D), torch.bfloat16, seed=1, scale=0.5)
+    mask = stk.make_streaming_mask(N, N, stk.StreamingMaskSpec(S, W), bm, bm, device=DEV)
+    out = stk.block_sparse_attention(q, k, v, mask, block_m=bm, block_n=bm, is_causal=True,
+                                     sink_size=S, window_size=W)
+    lse = _forward_lse(q, k, v, mask, bm, bm, S, W)
+    o_ref, lse_ref = cr.chunked_attention(q, k, v, mask, bm, bm, True, S, W)
+    _close(out, o_ref, torch.bfloat16, "c2 O")
+    _close(lse, lse_ref, torch.bfloat16, "c2 LSE")
+
+
+def _forward_lse(q, k, v, mask, bm, bn, S, W):
+    """LSE saved for backward by the autograd Function."""
+    leaves = [t.detach().requires_grad_(True) for t in (q, k, v)]
+    out = stk.block_sparse_attention(*leaves, mask, block_m=bm, block_n=bn, is_causal=True,
+                                     sink_size=S, window_size=W)
+    return out.grad_fn.saved_tensors[4]
+
+
+def test_config3_train_fp16_full():
+    B, H, N, D, S, W, bm = 4, 16, 8192, 64, 4, 1024, 64
+    q, k, v, do = _inputs((B, H, N, D), (B, H, N, D), torch.float16, seed=2, grad_out=True)
+    mask = stk.make_streaming_mask(N, N, stk.StreamingMaskSpec(S, W), bm, bm, device=DEV)
+    leaves = [t.clone().requires_grad_(True) for t in (q, k, v)]
+    out = stk.block_sparse_attention(*leaves, mask, block_m=bm, block_n=bm, is_causal=True,
+                                     sink_size=S, window_size=W)
+    out.backward(do)
+    ref = cr.chunked_attention(q, k, v, mask, bm, bm, True, S, W, do=do)
+    _close(out, ref[0], torch.float16, "c3 O")
+    for name, t, r in zip(("dQ", "dK", "dV"), leaves, ref[2:]):
+        _close(t.grad, r, torch.float16, f"c3 {name}")
+
+
+def test_config4_decode_bf16_full():
+    B, H, NKV, D, S, W = 8, 32, 100000, 128, 4, 2048
+    q, k, v, _ = _inputs((B, H, 1, D), (B, H, NKV, D), torch.bfloat16, seed=3, device_gen=True)
+    mask = stk.make_streaming_mask(1, NKV, stk.StreamingMaskSpec(S, W), 1, 64, device=DEV)
+    out = stk.block_sparse_attention(q, k, v, mask, block_m=1, block_n=64, is_causal=True,
+                                     sink_size=S, window_size=W)
+    o_ref, _ = cr.chunked_attention(q, k, v, mask, 1, 64, True, S, W)
+    _close(out, o_ref, torch.bfloat16, "c4 O")
+
+
+def test_config5_layer_bf16_full():
+    """One c5 attention layer (1x16x131072x64, S4 W4096, 128x64 blocks), fwd+bwd."""
+    B, H, N, D, S, W, bm, bn = 1, 16, 131072, 64, 4, 4096, 128, 64
+    q, k, v, do = _inputs((B, H, N, D), (B, H, N, D), torch.bfloat16, seed=4, device_gen=True,
+                          grad_out=True)
+    mask = stk.make_streaming_mask(N, N, stk.StreamingMaskSpec(S, W), bm, bn, device=DEV)
+    leaves = [t.clone().requires_grad_(True) for t in (q, k, v)]
+    out = stk.block_sparse_attention(*leaves, mask, block_m=bm, block_n=bn, is_causal=True,
+                                     sink_size=S, window_size=W)
+    out.backward(do)
+    ref = cr.chunked_attention(q, k, v, mask, bm, bn, True, S, W, do=do, chunk=2048)
+    _close(out, ref[0], torch.bfloat16, "c5 O")
+    for name, t, r in zip(("dQ", "dK", "dV"), leaves, ref[2:]):
+        _close(t.grad, r, torch.bfloat16, f"c5 {name}")
+
+
+def test_fwd_bwd_deterministic():
+    B, H, N, D, S, W = 2, 4, 2048, 64, 4, 256
+    q, k, v, do = _inputs((B, H, N, D), (B, H, N, D), torch.bfloat16, seed=9, grad_out=True)
+    mask = stk.make_streaming_mask(N, N, stk.StreamingMaskSpec(S, W), 64, 64, device=DEV)
+    runs = []
+    for _ in range(2):
+        leaves = [t.clone().requires_grad_(True) for t in (q, k, v)]
+        out = stk.block_sparse_attention(*leaves, mask, is_causal=True, sink_size=S, window_size=W)
+        out.backward(do)
+        runs.append([out.detach()] + [t.grad for t in leaves])
+    for a, b in zip(*runs):
+        assert torch.equal(a, b)

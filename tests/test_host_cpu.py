@@ -1,0 +1,133 @@
+"""CPU tests of the product's host side: mask API, validation errors, C ABI.
+
+No kernel is launched here (there is no GPU in this tier): the library is only
+loaded, its exported symbols checked against ``include/gki_bsa.h``, and its
+host-side argument validation exercised.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import sparse_triton_kernel as stk
+from gki import _lib
+from oracle import streaming_oracle as so
+
+from test_oracle_pins import BLOCK_SHAPES, TOKEN_SHAPES
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "gki_bsa.h"
+
+
+@pytest.mark.parametrize("n_q,n_kv,sink,window,bm,bn", BLOCK_SHAPES)
+def test_cpu_streaming_mask_matches_oracle(n_q, n_kv, sink, window, bm, bn):
+    m = stk.make_streaming_mask(n_q, n_kv, stk.StreamingMaskSpec(sink, window), bm, bn, device="cpu")
+    assert m.dtype == torch.int32 and m.is_contiguous()
+    np.testing.assert_array_equal(m.numpy(), so.block_mask(n_q, n_kv, sink, window, bm, bn))
+
+
+@pytest.mark.parametrize("n_q,n_kv,sink,window", TOKEN_SHAPES)
+def test_token_mask_matches_oracle(n_q, n_kv, sink, window):
+    np.testing.assert_array_equal(stk.streaming_token_mask(n_q, n_kv, sink, window).numpy(),
+                                  so.token_mask(n_q, n_kv, sink, window))
+
+
+def test_dense_mask_cpu():
+    np.testing.assert_array_equal(stk.make_dense_mask(64, 128, 16, 32, causal=True, device="cpu").numpy(),
+                                  so.dense_block_mask(64, 128, 16, 32, True))
+    assert stk.make_dense_mask(64, 128, 16, 32, device="cpu").all()
+    with pytest.raises(ValueError, match="must divide"):
+        stk.make_dense_mask(65, 128, 16, 32, device="cpu")
+
+
+def test_spec_and_mask_argument_errors():
+    with pytest.raises(ValueError, match="non-negative"):
+        stk.StreamingMaskSpec(-1, 4)
+    with pytest.raises(ValueError, match="non-negative"):
+        stk.StreamingMaskSpec(4, -4)
+    with pytest.raises(ValueError, match="positive"):
+        stk.make_streaming_mask(0, 10, stk.StreamingMaskSpec(1, 1), 4, 4, device="cpu")
+    with pytest.raises(ValueError, match="positive"):
+        stk.make_streaming_mask(10, 10, stk.StreamingMaskSpec(1, 1), 0, 4, device="cpu")
+
+
+def test_reference_eager_api_matches_oracle():
+    n_q, n_kv, D, S, W, bm, bn = 48, 80, 16, 2, 20, 16, 16
+    g = torch.Generator().manual_seed(0)
+    q, k, v = (torch.randn(1, 2, n, D, generator=g, dtype=torch.float64) for n in (n_q, n_kv, n_kv))
+    mask = stk.make_streaming_mask(n_q, n_kv, stk.StreamingMaskSpec(S, W), bm, bn, device="cpu")
+    out = stk.reference_block_sparse_attention(q, k, v, mask, block_m=bm, block_n=bn,
+                                               is_causal=True, sink_size=S, window_size=W)
+    eff = so.effective_mask(mask.numpy(), n_q, n_kv, bm, bn, True, S, W)
+    np.testing.assert_allclose(out.numpy(), so.attention_fwd(q.numpy(), k.numpy(), v.numpy(), eff)[0],
+                               atol=1e-12)
+
+
+def _qkv(device="cpu", dtype=torch.float32, shape=(1, 2, 32, 16)):
+    return [torch.zeros(shape, dtype=dtype, device=device) for _ in range(3)]
+
+
+def test_op_validation_errors_on_cpu():
+    q, k, v = _qkv()
+    mask = torch.ones(1, 1, dtype=torch.int32)
+    with pytest.raises(ValueError, match="4-D"):
+        stk.block_sparse_attention(q[0], k, v, mask)
+    with pytest.raises(ValueError, match="CUDA device"):
+        stk.block_sparse_attention(q, k, v, mask, block_m=32, block_n=32)
+
+
+def _declared_symbols():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(gki_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = _declared_symbols()
+    assert len(names) >= 13
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in gki_bsa.h but not exported"
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+    assert set(_lib.SIGNATURES) == set(names)
+    assert lib.gki_abi_version() == 1
+
+
+def test_tile_sizes():
+    ts = _lib.tile_sizes()
+    assert ts == {"tile_m": 64, "tile_n": 64, "decode_tile_m": 16, "decode_max_q": 4,
+                  "decode_max_tokens": 512}
+
+
+def test_capi_rejects_bad_arguments_before_launch():
+    lib = _lib.load()
+    null = ctypes.c_void_p(0)
+    # unsupported head_dim: code 2, nothing launched
+    rc = lib.gki_bsa_fwd(1, 1, 1, 1, 1, 2, 1, 1, 64, 64, 48, 1, 1, 1, 1, 1, 1, 64, 64, 0.1, 1, 4, 8,
+                         null)
+    assert rc == 2 and b"head_dim" in lib.gki_last_error()
+    # bad dtype code
+    rc = lib.gki_bsa_fwd(1, 1, 1, 1, 1, 7, 1, 1, 64, 64, 64, 1, 1, 1, 1, 1, 1, 64, 64, 0.1, 1, 4, 8,
+                         null)
+    assert rc == 2 and b"dtype" in lib.gki_last_error()
+    # mask shape mismatch
+    rc = lib.gki_bsa_fwd(1, 1, 1, 1, 1, 0, 1, 1, 64, 64, 64, 1, 1, 1, 1, 2, 1, 64, 64, 0.1, 1, 4, 8,
+                         null)
+    assert rc == 1 and b"mask shape" in lib.gki_last_error()
+    # schedule row count mismatch
+    rc = lib.gki_bsa_fwd(1, 1, 1, 1, 1, 0, 1, 1, 200, 64, 64, 1, 1, 2, 1, 4, 1, 64, 64, 0.1, 1, 4, 8,
+                         null)
+    assert rc == 1 and b"schedule" in lib.gki_last_error()
+    # decode: too many rows
+    rc = lib.gki_bsa_decode(1, 1, 1, 1, 1, 2, 1, 1, 8, 64, 64, 1, 1, 1, 1, 1, 64, 64, 0.1, 1, 4, 8,
+                            1, 1, null)
+    assert rc == 2 and b"decode" in lib.gki_last_error()
+    # masks
+    assert lib.gki_streaming_mask(1, 0, 10, 4, 4, 64, 64, null) == 1
+    assert lib.gki_dense_mask(1, 60, 64, 16, 16, 0, null) == 1
+    assert b"divide" in lib.gki_last_error()
+    assert lib.gki_bsa_decode_workspace_floats(2, 3, 1, 128, 5) == 2 * 3 * 5 * 130
