@@ -1,0 +1,336 @@
+#!/usr/bin/env python
+"""Benchmark of the gfx950 block-sparse StreamingLLM attention on one MI355X.
+
+Metric: kept-block TFLOP/s for forward / backward and decode-step
+KV GB/s, each as a fraction of the MI355X roofline.
+
+* ``value`` -- config 2 (``configs[1]``): prefill forward, B1 H32 N16384 D128
+  bf16, S4 W2048, 64x64 blocks, causal. One step = one forward call.
+  Kept-block flops = 4 * 64 * 64 * 128 per kept tile per (b, h).
+* ``train``  -- config 3: fwd + bwd, B4 H16 N8192 D64 fp16, S4 W1024
+  (fwd 4*BM*BN*D, bwd 10*BM*BN*D per kept tile).
+* ``decode`` -- config 4: B8 H32, one query, KV 100000, D128 bf16, S4 W2048;
+  token-exact kept K/V bytes (S+W)*D*2*2 per (b, h) over the step time.
+* ``layer_c5`` -- one config-5 attention layer (1x16x131072x64 bf16, S4 W4096,
+  128x64 blocks), fwd + bwd.
+* ``cpu_baseline`` -- the reference's eager masked attention (restated in
+  ``oracle/eager_cpu.py``) in fp32 on the host cores, on a bounded sample of
+  config 2 (whole heads until ~10 s of CPU time), in the same unit.
+
+Inputs are synthetic N(0, 1) (config 2 scaled by 0.5), generated once and
+resident in HBM before the timed region. Kernel durations come from HIP
+events recorded on the stream the kernels run on (torch's current stream).
+Prints ONE JSON line on stdout; progress goes to stderr.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT / "graph-kernel-injection_amd", ROOT):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+METRIC = "kept-block TFLOP/s fwd/bwd + decode-step KV GB/s as % of MI355X roofline"
+PEAK_MFMA_16 = 2500.0   # TFLOP/s, dense bf16/fp16 MFMA
+PEAK_HBM = 8000.0       # GB/s
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def _randn(shape, gen, scale, dtype, device):
+    import torch
+
+    return (torch.randn(shape, generator=gen, dtype=torch.float32) * scale).to(dtype).to(device)
+
+
+def _time_calls(fn, steps: int, warmup: int):
+    """Warm up, then time ``steps`` calls; returns (per-call ms list, total ms)."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(steps)]
+    t_all0, t_all1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t_all0.record()
+    for a, b in evs:
+        a.record()
+        fn()
+        b.record()
+    t_all1.record()
+    torch.cuda.synchronize()
+    return [a.elapsed_time(b) for a, b in evs], t_all0.elapsed_time(t_all1)
+
+
+def _roofline(achieved: float, peak: float, unit: str, bound: str, traffic=None) -> dict:
+    return {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": traffic}
+
+
+def section_c2(steps: int, warmup: int, keep_cpu_inputs: bool):
+    import torch
+
+    import sparse_triton_kernel as stk
+
+    B, H, N, D, S, W, bm = 1, 32, 16384, 128, 4, 2048, 64
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(1)
+    q32, k32, v32 = (torch.randn(B, H, N, D, generator=g) * 0.5 for _ in range(3))
+    q, k, v = (t.to(torch.bfloat16).to(dev) for t in (q32, k32, v32))
+    mask = stk.make_streaming_mask(N, N, stk.StreamingMaskSpec(S, W), bm, bm, device=dev)
+    kept = int(mask.sum().item())
+    flops = 4.0 * bm * bm * D * kept * B * H
+
+    def fn():
+        return stk.block_sparse_attention(q, k, v, mask, block_m=bm, block_n=bm, is_causal=True,
+                                          sink_size=S, window_size=W)
+
+    per, total = _time_calls(fn, steps, warmup)
+    avg = statistics.mean(per)
+    tflops = flops / (avg * 1e-3) / 1e12
+    log(f"[c2] fwd kernel avg {avg:.4f} ms (p50 {statistics.median(per):.4f}), "
+        f"{tflops:.1f} TFLOP/s, step {total / steps:.4f} ms")
+    cpu_inputs = None
+    if keep_cpu_inputs:
+        cpu_inputs = tuple(t.to(torch.bfloat16).float() for t in (q32, k32, v32)) + (mask.cpu(),)
+    del q, k, v
+    return {
+        "kept_tiles": kept, "flops_per_step": flops, "avg_ms": avg, "p50_ms": statistics.median(per),
+        "ms_per_step": total / steps, "tflops": tflops,
+    }, cpu_inputs
+
+
+def section_c3(steps: int, warmup: int) -> dict:
+    import torch
+
+    import sparse_triton_kernel as stk
+
+    B, H, N, D, S, W, bm = 4, 16, 8192, 64, 4, 1024, 64
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(2)
+    q, k, v, do = (_randn((B, H, N, D), g, 1.0, torch.float16, dev) for _ in range(4))
+    q, k, v = (t.requires_grad_(True) for t in (q, k, v))
+    mask = stk.make_streaming_mask(N, N, stk.StreamingMaskSpec(S, W), bm, bm, device=dev)
+    kept = int(mask.sum().item())
+    f_fwd = 4.0 * bm * bm * D * kept * B * H
+    f_bwd = 10.0 * bm * bm * D * kept * B * H
+    evs = []
+
+    def one():
+        for t in (q, k, v):
+            t.grad = None
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        e[0].record()
+        out = stk.block_sparse_attention(q, k, v, mask, is_causal=True, sink_size=S, window_size=W)
+        e[1].record()
+        out.backward(do)
+        e[2].record()
+        evs.append(e)
+
+    for _ in range(warmup):
+        one()
+    torch.cuda.synchronize()
+    evs.clear()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        one()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    fwd = statistics.mean(e[0].elapsed_time(e[1]) for e in evs)
+    bwd = statistics.mean(e[1].elapsed_time(e[2]) for e in evs)
+    res = {
+        "workload": "c3 training fwd+bwd: B4 H16 N8192 D64 fp16, S4 W1024, 64x64 blocks, causal",
+        "kept_tiles": kept, "fwd_ms": fwd, "bwd_ms": bwd, "ms_per_step": wall,
+        "fwd_tflops": f_fwd / (fwd * 1e-3) / 1e12, "bwd_tflops": f_bwd / (bwd * 1e-3) / 1e12,
+        "fwdbwd_tflops": (f_fwd + f_bwd) / ((fwd + bwd) * 1e-3) / 1e12,
+    }
+    res["roofline"] = _roofline(res["fwdbwd_tflops"], PEAK_MFMA_16, "TFLOP/s", "mfma")
+    log(f"[c3] fwd {fwd:.4f} ms ({res['fwd_tflops']:.1f} TF/s), bwd {bwd:.4f} ms "
+        f"({res['bwd_tflops']:.1f} TF/s)")
+    return res
+
+
+def section_c4(steps: int, warmup: int) -> dict:
+    import torch
+
+    import sparse_triton_kernel as stk
+
+    B, H, NKV, D, S, W = 8, 32, 100000, 128, 4, 2048
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(3)
+    q = torch.randn(B, H, 1, D, generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn(B, H, NKV, D, generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn(B, H, NKV, D, generator=g, device=dev).to(torch.bfloat16)
+    mask = stk.make_streaming_mask(1, NKV, stk.StreamingMaskSpec(S, W), 1, 64, device=dev)
+    kept = int(mask.sum().item())
+    exact_bytes = (S + W) * D * 2 * 2 * B * H
+    block_bytes = kept * 64 * D * 2 * 2 * B * H
+
+    def fn():
+        return stk.block_sparse_attention(q, k, v, mask, block_m=1, block_n=64, is_causal=True,
+                                          sink_size=S, window_size=W)
+
+    per, total = _time_calls(fn, steps, warmup)
+    avg = statistics.mean(per)
+    gbs = exact_bytes / (avg * 1e-3) / 1e9
+    res = {
+        "workload": "c4 decode step: B8 H32 n_q=1 KV100000 D128 bf16, S4 W2048, BM=1 BN=64",
+        "kept_tiles": kept, "kv_bytes_token_exact": exact_bytes, "kv_bytes_block_granular": block_bytes,
+        "avg_ms": avg, "p50_ms": statistics.median(per), "ms_per_step": total / steps,
+        "kv_gbs": gbs, "kv_gbs_block_granular": block_bytes / (avg * 1e-3) / 1e9,
+    }
+    res["roofline"] = _roofline(gbs, PEAK_HBM, "GB/s", "hbm")
+    log(f"[c4] decode step {avg * 1e3:.2f} us, {gbs:.0f} GB/s token-exact "
+        f"({100 * gbs / PEAK_HBM:.1f}% of HBM peak)")
+    del k, v
+    return res
+
+
+def section_c5(steps: int, warmup: int) -> dict:
+    import torch
+
+    import sparse_triton_kernel as stk
+
+    B, H, N, D, S, W, bm, bn = 1, 16, 131072, 64, 4, 4096, 128, 64
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(4)
+    q, k, v, do = (torch.randn(B, H, N, D, generator=g, device=dev).to(torch.bfloat16) for _ in range(4))
+    q, k, v = (t.requires_grad_(True) for t in (q, k, v))
+    mask = stk.make_streaming_mask(N, N, stk.StreamingMaskSpec(S, W), bm, bn, device=dev)
+    kept = int(mask.sum().item())
+    f_fwd = 4.0 * bm * bn * D * kept * B * H
+    f_bwd = 10.0 * bm * bn * D * kept * B * H
+    evs = []
+
+    def one():
+        for t in (q, k, v):
+            t.grad = None
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        e[0].record()
+        out = stk.block_sparse_attention(q, k, v, mask, block_m=bm, block_n=bn, is_causal=True,
+                                         sink_size=S, window_size=W)
+        e[1].record()
+        out.backward(do)
+        e[2].record()
+        evs.append(e)
+
+    for _ in range(warmup):
+        one()
+    torch.cuda.synchronize()
+    evs.clear()
+    for _ in range(steps):
+        one()
+    torch.cuda.synchronize()
+    fwd = statistics.mean(e[0].elapsed_time(e[1]) for e in evs)
+    bwd = statistics.mean(e[1].elapsed_time(e[2]) for e in evs)
+    res = {
+        "workload": "c5 attention layer fwd+bwd: B1 H16 N131072 D64 bf16, S4 W4096, 128x64 blocks",
+        "kept_tiles": kept, "fwd_ms": fwd, "bwd_ms": bwd,
+        "fwd_tflops": f_fwd / (fwd * 1e-3) / 1e12, "bwd_tflops": f_bwd / (bwd * 1e-3) / 1e12,
+        "fwdbwd_tflops": (f_fwd + f_bwd) / ((fwd + bwd) * 1e-3) / 1e12,
+        "attention_ms_12_layers": 12 * (fwd + bwd),
+    }
+    res["roofline"] = _roofline(res["fwdbwd_tflops"], PEAK_MFMA_16, "TFLOP/s", "mfma")
+    log(f"[c5] layer fwd {fwd:.3f} ms, bwd {bwd:.3f} ms ({res['fwdbwd_tflops']:.1f} TF/s)")
+    return res
+
+
+def cpu_baseline(cpu_inputs, kept: int, budget_s: float) -> dict:
+    """Reference eager path (fp32, all host threads) on whole heads of config 2."""
+    import torch
+
+    from oracle.eager_cpu import eager_masked_attention
+
+    q, k, v, mask = cpu_inputs
+    H, D = q.shape[1], q.shape[-1]
+    threads = torch.get_num_threads()
+    heads = 0
+    t0 = time.perf_counter()
+    while heads < H:
+        sl = slice(heads, heads + 1)
+        eager_masked_attention(q[:, sl], k[:, sl], v[:, sl], mask, 64, 64, True, 4, 2048)
+        heads += 1
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    elapsed = time.perf_counter() - t0
+    flops = 4.0 * 64 * 64 * D * kept * heads
+    tflops = flops / elapsed / 1e12
+    log(f"[cpu] eager fp32 on {threads} threads: {heads} head(s) in {elapsed:.1f} s, "
+        f"{tflops * 1e3:.2f} GFLOP/s kept-block")
+    return {"value": round(tflops, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": (f"config 2 forward, {heads} of {H} heads (B1 N16384 D128, fp32 eager "
+                       f"masked attention over all keys, 2048-row chunks), {elapsed:.1f} s; "
+                       f"full-step extrapolation {elapsed * H / heads:.1f} s")}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--sections", default="c2,c3,c4,c5,cpu",
+                    help="comma list among c2,c3,c4,c5,cpu (c2 is always run)")
+    ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline work")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(f"bench.py measures one MI355X only; --gpus {args.gpus} is not supported "
+              "(the op has no multi-GPU path in this build).", file=sys.stderr)
+        return 2
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU (none visible)", file=sys.stderr)
+        return 2
+    sections = set(s.strip() for s in args.sections.split(","))
+    c2, cpu_in = section_c2(args.steps, args.warmup, "cpu" in sections)
+    line = {
+        "metric": METRIC,
+        "value": round(c2["tflops"], 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(c2["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: Q/K/V ~ N(0,1)*0.5 from a seed-1 CPU generator (no dataset)",
+        "config": {
+            "workload": "c2 prefill forward: B1 H32 N16384 D128 bf16, StreamingLLM S4 W2048, "
+                        "64x64 blocks, causal",
+            "kept_tiles": c2["kept_tiles"], "flops_per_step": c2["flops_per_step"],
+            "kernel_avg_ms": round(c2["avg_ms"], 5), "kernel_p50_ms": round(c2["p50_ms"], 5),
+        },
+        "roofline": _roofline(c2["tflops"], PEAK_MFMA_16, "TFLOP/s", "mfma"),
+    }
+    torch.cuda.empty_cache()
+    if "c3" in sections:
+        line["train"] = section_c3(args.steps, args.warmup)
+        torch.cuda.empty_cache()
+    if "c4" in sections:
+        line["decode"] = section_c4(args.steps, args.warmup)
+        torch.cuda.empty_cache()
+    if "c5" in sections:
+        line["layer_c5"] = section_c5(max(3, args.steps // 4), 2)
+        torch.cuda.empty_cache()
+    if "cpu" in sections:
+        line["cpu_baseline"] = cpu_baseline(cpu_in, c2["kept_tiles"], args.cpu_budget)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

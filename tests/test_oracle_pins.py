@@ -300,3 +300,15 @@ def test_chunked_reference_matches_dense_oracle(causal):
     np.testing.assert_allclose(res[1].numpy(), lse, atol=1e-12)
     for ours, ref in zip(res[2:], grads):
         np.testing.assert_allclose(ours.numpy(), ref, atol=1e-11)
+
+
+def test_eager_cpu_baseline_matches_oracle():
+    from oracle import eager_cpu
+
+    B, H, n_q, n_kv, D, bm, bn, S, W = 1, 2, 150, 200, 16, 32, 16, 3, 40
+    m = so.block_mask(n_q, n_kv, S, W, bm, bn)
+    q, k, v = _rand((B, H, n_q, D), 30), _rand((B, H, n_kv, D), 31), _rand((B, H, n_kv, D), 32)
+    got = eager_cpu.eager_masked_attention(*(torch.from_numpy(x) for x in (q, k, v)),
+                                           torch.from_numpy(m), bm, bn, True, S, W, chunk=64)
+    ref, _ = so.attention_fwd(q, k, v, so.effective_mask(m, n_q, n_kv, bm, bn, True, S, W))
+    np.testing.assert_allclose(got.numpy(), ref, atol=1e-12)
