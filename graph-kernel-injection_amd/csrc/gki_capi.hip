@@ -33,10 +33,11 @@ int bwd_dispatch(int dtype, int head_dim, const Geom& g, const void* q, const vo
                  float* delta, const int32_t* row_ptr, const int32_t* row_idx, int n_qt,
                  const int32_t* col_ptr, const int32_t* col_idx, const int32_t* order, int n_heavy,
                  int n_kt, hipStream_t stream);
+int decode_tokens_dispatch(const Geom& g, const int32_t* list, int n_ent, int32_t* tok, int32_t* count,
+                           hipStream_t stream);
 int decode_dispatch(int dtype, int head_dim, const Geom& g, const void* q, const void* k, const void* v,
-                    void* o, float* lse, const int32_t* list, int n_ent, float* ws, int n_splits,
+                    void* o, float* lse, const int32_t* tok, int n_tokens, float* ws, int n_splits,
                     hipStream_t stream);
-int decode_max_tokens_per_split();
 
 namespace {
 
@@ -48,6 +49,7 @@ int make_geom(Geom& g, int dtype, int B, int H, int n_q, int n_kv, int head_dim,
   GKI_REQUIRE(head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128, 2,
               "unsupported head_dim " + std::to_string(head_dim) + " (supported: 16, 32, 64, 128)");
   GKI_REQUIRE(B > 0 && H > 0 && n_q > 0 && n_kv > 0, 1, "B, H, n_q and n_kv must be positive");
+  GKI_REQUIRE((int64_t)B * H < (1ll << 31) / 4096, 1, "B * H too large");
   GKI_REQUIRE(block_m > 0 && block_n > 0, 1, "block_m and block_n must be positive");
   GKI_REQUIRE(n_qb == (n_q + block_m - 1) / block_m && n_kb == (n_kv + block_n - 1) / block_n, 1,
               "block mask shape does not match ceil(n_q/block_m) x ceil(n_kv/block_n)");
@@ -83,13 +85,11 @@ int gki_abi_version(void) { return 1; }
 
 const char* gki_last_error(void) { return g_last_error.c_str(); }
 
-int gki_tile_sizes(int32_t* tile_m, int32_t* tile_n, int32_t* decode_tile_m, int32_t* decode_max_q,
-                   int32_t* decode_max_tokens) {
+int gki_tile_sizes(int32_t* tile_m, int32_t* tile_n, int32_t* decode_tile_m, int32_t* decode_max_q) {
   if (tile_m) *tile_m = kTileM;
   if (tile_n) *tile_n = kTileN;
   if (decode_tile_m) *decode_tile_m = kDecodeTileM;
   if (decode_max_q) *decode_max_q = kDecodeMaxQ;
-  if (decode_max_tokens) *decode_max_tokens = decode_max_tokens_per_split();
   return 0;
 }
 
@@ -132,9 +132,22 @@ int64_t gki_bsa_decode_workspace_floats(int32_t B, int32_t H, int32_t n_q, int32
   return (int64_t)B * H * n_splits * n_q * (head_dim + 2);
 }
 
+int gki_decode_tokens(const int32_t* tile_list, int32_t n_tiles, int32_t n_q, int32_t n_kv,
+                      const int32_t* mask, int32_t n_qb, int32_t n_kb, int32_t block_m, int32_t block_n,
+                      int32_t is_causal, int32_t sink_size, int32_t window_size, int32_t* tokens,
+                      int32_t* n_tokens, void* stream) {
+  Geom g;
+  if (int rc = make_geom(g, kBF16, 1, 1, n_q, n_kv, 64, mask, n_qb, n_kb, block_m, block_n, 1.f,
+                         is_causal, sink_size, window_size))
+    return rc;
+  GKI_REQUIRE(n_tokens && (n_tiles == 0 || (tile_list && tokens)), 1, "gki_decode_tokens: null pointer");
+  GKI_REQUIRE(n_tiles >= 0, 1, "gki_decode_tokens: negative tile count");
+  return decode_tokens_dispatch(g, tile_list, n_tiles, tokens, n_tokens, (hipStream_t)stream);
+}
+
 int gki_bsa_decode(const void* q, const void* k, const void* v, void* o, float* lse, int32_t dtype,
                    int32_t B, int32_t H, int32_t n_q, int32_t n_kv, int32_t head_dim,
-                   const int32_t* tile_list, int32_t n_tiles, const int32_t* mask, int32_t n_qb,
+                   const int32_t* tokens, int32_t n_tokens, const int32_t* mask, int32_t n_qb,
                    int32_t n_kb, int32_t block_m, int32_t block_n, float softmax_scale,
                    int32_t is_causal, int32_t sink_size, int32_t window_size, float* workspace,
                    int32_t n_splits, void* stream) {
@@ -142,13 +155,13 @@ int gki_bsa_decode(const void* q, const void* k, const void* v, void* o, float* 
   if (int rc = make_geom(g, dtype, B, H, n_q, n_kv, head_dim, mask, n_qb, n_kb, block_m, block_n,
                          softmax_scale, is_causal, sink_size, window_size))
     return rc;
-  GKI_REQUIRE(q && k && v && o && lse && workspace, 1, "gki_bsa_decode: null pointer");
+  GKI_REQUIRE(q && k && v && o && lse, 1, "gki_bsa_decode: null pointer");
+  GKI_REQUIRE(n_splits == 1 || workspace, 1, "gki_bsa_decode: null workspace");
   GKI_REQUIRE(n_q <= kDecodeMaxQ, 2, "gki_bsa_decode: n_q exceeds the decode kernel's row limit");
-  GKI_REQUIRE(n_tiles >= 0 && (n_tiles == 0 || tile_list), 1, "gki_bsa_decode: bad tile list");
-  GKI_REQUIRE(n_splits >= 1, 1, "gki_bsa_decode: n_splits must be >= 1");
-  GKI_REQUIRE((int64_t)n_tiles * kTileN <= (int64_t)n_splits * decode_max_tokens_per_split(), 1,
-              "gki_bsa_decode: too few splits for the kept-token count");
-  return decode_dispatch(dtype, head_dim, g, q, k, v, o, lse, tile_list, n_tiles, workspace, n_splits,
+  GKI_REQUIRE(n_tokens >= 0 && (n_tokens == 0 || tokens), 1, "gki_bsa_decode: bad token list");
+  GKI_REQUIRE(n_splits >= 1 && (int64_t)n_splits * B * H < (1ll << 31), 1,
+              "gki_bsa_decode: n_splits must be >= 1 and the grid must fit");
+  return decode_dispatch(dtype, head_dim, g, q, k, v, o, lse, tokens, n_tokens, workspace, n_splits,
                          (hipStream_t)stream);
 }
 

@@ -5,16 +5,23 @@
 // mask entries and does a 1-row tl.dot per kept tile. Here the decode step
 // (n_q <= 4 query rows at the end of the KV cache, q_offset = n_kv - n_q) is a
 // bandwidth-bound split-KV pass:
-//   * the kept kv tiles of the single q tile come from the GPU-resident list;
-//     inside each tile only the hull of visible tokens is read (sink prefix,
-//     window suffix, in-bounds rows), so the K/V bytes read are token-exact for
-//     n_q = 1 (S + W rows per head when they do not overlap);
-//   * that token stream is cut into n_splits equal pieces; workgroup
-//     (bh, split) streams its piece with 16-byte coalesced loads (D/8 lanes per
-//     row), computes exact scores, a local softmax and P V, and writes
-//     (acc[D], m, l) to a workspace;
-//   * combine_kernel merges the splits: O = sum acc_s 2^(m_s-M) / sum l_s 2^(m_s-M),
-//     LSE = M ln2 + ln L, with the (O = 0, LSE = 0) sentinel for empty rows.
+//   * decode_tokens_kernel (once per mask, cached by the host) expands the kept
+//     kv tiles of the single decode q tile into the positions of the tokens any
+//     query row can see (the hull of sink prefix / window suffix / in-bounds
+//     rows of each tile): S + W positions per head for n_q = 1;
+//   * decode_kernel: workgroup (bh, split) takes an equal slice of that stream
+//     and each of its 16 waves streams a contiguous 1/16 of the slice in
+//     rounds of 8 token-row passes: all 16-byte K and V loads of a round are
+//     issued together (D/8 lanes per row, non-temporal), then scores, a
+//     wave-local online softmax and P V. No barrier until the end, where the
+//     waves merge in LDS. With one split per head the workgroup writes O and
+//     LSE itself; otherwise it writes (acc[D], m, l) to a workspace and
+//   * combine_kernel (one wave per row) merges the splits:
+//     O = sum acc_s 2^(m_s-M) / sum l_s 2^(m_s-M), LSE = M ln2 + ln L,
+//     with the (O = 0, LSE = 0) sentinel for empty rows.
+// Cross-workgroup merging goes through a second launch on purpose: publishing
+// partials across XCDs inside one kernel needs agent-scope fences, which on
+// gfx950 write back and invalidate L2.
 // Numerics follow the reference forward: fp32 scores scaled after the dot, P
 // cast to V's dtype before P V, token mask causal & (sink | window).
 #include "gki_common.cuh"
@@ -22,44 +29,6 @@
 namespace gki {
 namespace {
 
-constexpr int kMaxTok = 512;   // tokens per split held in LDS
-
-__device__ inline float block_max(float v, float* red) {
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
-  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-}
-__device__ inline float block_sum(float v, float* red) {
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
-  return (red[0] + red[1]) + (red[2] + red[3]);
-}
-__device__ inline int block_sum_i(int v, int* red) {
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
-  return (red[0] + red[1]) + (red[2] + red[3]);
-}
-// Exclusive block scan of one int per thread.
-__device__ inline int block_excl_scan(int v, int* red) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int inc = v;
-  for (int off = 1; off < 64; off <<= 1) {
-    const int u = __shfl_up(inc, off);
-    if (lane >= off) inc += u;
-  }
-  __syncthreads();
-  if (lane == 63) red[wave] = inc;
-  __syncthreads();
-  int before = 0;
-  for (int w = 0; w < wave; ++w) before += red[w];
-  return before + inc - v;
-}
 
 // Hull [lo, hi) of the tokens of kv tile `kt` visible to any of the n_q rows.
 __device__ inline void tile_hull(const Geom& g, int kt, int& lo, int& hi) {
@@ -87,43 +56,17 @@ __device__ inline void tile_hull(const Geom& g, int kt, int& lo, int& hi) {
   }
 }
 
-template <typename T, int D, int NQ>
-__global__ __launch_bounds__(256) void decode_kernel(Geom g, const typename T::storage* __restrict__ Q,
-                                                     const typename T::storage* __restrict__ K,
-                                                     const typename T::storage* __restrict__ V,
-                                                     float* __restrict__ ws,
-                                                     const int32_t* __restrict__ list, int n_ent,
-                                                     int n_splits) {
-  using S = typename T::storage;
-  constexpr int VEC = 16 / sizeof(S);
-  constexpr int LPT = D / VEC;     // lanes per token row
-  constexpr int TPP = 256 / LPT;   // token rows per pass
-  constexpr int UNR = 4;
-  __shared__ float sc[NQ][kMaxTok];
-  __shared__ int pos[kMaxTok];
-  __shared__ float accbuf[4][NQ][D];
-  __shared__ float redf[4];
-  __shared__ int redi[4];
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int split = blockIdx.x % n_splits, bh = blockIdx.x / n_splits;
-  const size_t qb = (size_t)bh * g.n_q * D;
-  const size_t kb = (size_t)bh * g.n_kv * D;
-
-  // --- token stream of this split -------------------------------------------
-  int local = 0;
-  for (int e = tid; e < n_ent; e += 256) {
-    int lo, hi;
-    tile_hull(g, list[e] & kIdxMask, lo, hi);
-    local += hi - lo;
-  }
-  const int total = block_sum_i(local, redi);
-  const int s0 = (int)(((int64_t)total * split) / n_splits);
-  const int s1 = (int)(((int64_t)total * (split + 1)) / n_splits);
-  const int n_tok = s1 - s0;
-  int base = 0;
+// One workgroup: tile list -> token positions (| partial << 30) and their count.
+__global__ __launch_bounds__(256) void decode_tokens_kernel(Geom g, const int32_t* __restrict__ list,
+                                                            int n_ent, int32_t* __restrict__ tok,
+                                                            int32_t* __restrict__ count) {
+  __shared__ int red[4];
+  __shared__ int carry;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (threadIdx.x == 0) carry = 0;
+  __syncthreads();
   for (int c = 0; c < n_ent; c += 256) {
-    const int e = c + tid;
+    const int e = c + threadIdx.x;
     int lo = 0, hi = 0, flag = 0;
     if (e < n_ent) {
       const int ent = list[e];
@@ -131,39 +74,91 @@ __global__ __launch_bounds__(256) void decode_kernel(Geom g, const typename T::s
       flag = (ent >> kPartialBit) & 1;
     }
     const int len = hi - lo;
-    const int start = base + block_excl_scan(len, redi);
-    const int a = max(start, s0), z = min(start + len, s1);
-    for (int t = a; t < z; ++t) pos[t - s0] = (lo + t - start) | (flag << kPartialBit);
-    base += block_sum_i(len, redi);
+    int inc = len;
+    for (int off = 1; off < 64; off <<= 1) {
+      const int u = __shfl_up(inc, off);
+      if (lane >= off) inc += u;
+    }
+    if (lane == 63) red[wave] = inc;
+    __syncthreads();
+    int start = carry;
+    for (int w = 0; w < wave; ++w) start += red[w];
+    start += inc - len;
+    for (int t = 0; t < len; ++t) tok[start + t] = (lo + t) | (flag << kPartialBit);
+    __syncthreads();
+    if (threadIdx.x == 0) carry += red[0] + red[1] + red[2] + red[3];
+    __syncthreads();
   }
-  __syncthreads();
+  if (threadIdx.x == 0) *count = carry;
+}
 
-  // --- scores ----------------------------------------------------------------
-  const int tk = tid / LPT, ch = tid % LPT;
+constexpr int kDecodeWaves = 16;   // one 1024-thread workgroup per (b, h, split)
+
+template <typename T, int D, int NQ>
+__global__ __launch_bounds__(64 * kDecodeWaves) void decode_kernel(
+    Geom g, const typename T::storage* __restrict__ Q, const typename T::storage* __restrict__ K,
+    const typename T::storage* __restrict__ V, typename T::storage* __restrict__ O,
+    float* __restrict__ LSE, float* __restrict__ ws, const int32_t* __restrict__ tok, int n_tokens,
+    int n_splits) {
+  using S = typename T::storage;
+  constexpr int VEC = 16 / sizeof(S);
+  constexpr int LPT = D / VEC;      // lanes per token row
+  constexpr int TPW = 64 / LPT;     // token rows per wave pass
+  constexpr int NU = 8;             // passes per round (16-byte K and V loads in flight per lane)
+  constexpr int RT = NU * TPW;      // tokens per wave round
+  constexpr int NW = kDecodeWaves;
+  __shared__ float wm[NW][NQ], wl[NW][NQ];
+  __shared__ float wacc[NW][NQ][D];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int split = blockIdx.x % n_splits, bh = blockIdx.x / n_splits;
+  const size_t qb = (size_t)bh * g.n_q * D;
+  const size_t kb = (size_t)bh * g.n_kv * D;
+  // this workgroup's slice of the token stream, then this wave's contiguous part
+  const int g0 = (int)(((int64_t)n_tokens * split) / n_splits);
+  const int g1 = (int)(((int64_t)n_tokens * (split + 1)) / n_splits);
+  const int w0 = g0 + (int)(((int64_t)(g1 - g0) * wave) / NW);
+  const int w1 = g0 + (int)(((int64_t)(g1 - g0) * (wave + 1)) / NW);
+  const int tk = lane / LPT, ch = lane % LPT;
+
   float qv[NQ][VEC];
 #pragma unroll
   for (int r = 0; r < NQ; ++r) {
-    if (r < g.n_q) {
-      const uint4 raw = *(const uint4*)(Q + qb + (size_t)r * D + ch * VEC);
-      const S* e = (const S*)&raw;
+    uint4 raw = make_uint4(0, 0, 0, 0);
+    if (r < g.n_q) raw = *(const uint4*)(Q + qb + (size_t)r * D + ch * VEC);
+    const S* e = (const S*)&raw;
 #pragma unroll
-      for (int i = 0; i < VEC; ++i) qv[r][i] = T::to_float(e[i]);
-    } else {
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) qv[r][i] = 0.f;
-    }
+    for (int i = 0; i < VEC; ++i) qv[r][i] = T::to_float(e[i]);
   }
-  for (int j0 = 0; j0 < n_tok; j0 += TPP * UNR) {
-    uint4 kr[UNR];
+  // wave-local online softmax state; m is uniform across the wave, l and acc
+  // are per token-row group and summed at the end
+  float m[NQ], l[NQ], acc[NQ][VEC];
 #pragma unroll
-    for (int u = 0; u < UNR; ++u) {
-      const int j = j0 + u * TPP + tk;
-      kr[u] = j < n_tok ? ld_nt16(K + kb + (size_t)(pos[j] & kIdxMask) * D + ch * VEC)
-                        : make_uint4(0, 0, 0, 0);
+  for (int r = 0; r < NQ; ++r) {
+    m[r] = kNegInf;
+    l[r] = 0.f;
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) acc[r][i] = 0.f;
+  }
+
+  for (int t0 = w0; t0 < w1; t0 += RT) {
+    int pj[NU];
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      const int t = t0 + u * TPW + tk;
+      pj[u] = t < w1 ? tok[t] : -1;
     }
+    uint4 kr[NU], vr[NU];
 #pragma unroll
-    for (int u = 0; u < UNR; ++u) {
-      const int j = j0 + u * TPP + tk;
+    for (int u = 0; u < NU; ++u)
+      kr[u] = pj[u] >= 0 ? ld_nt16(K + kb + (size_t)(pj[u] & kIdxMask) * D + ch * VEC) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int u = 0; u < NU; ++u)
+      vr[u] = pj[u] >= 0 ? ld_nt16(V + kb + (size_t)(pj[u] & kIdxMask) * D + ch * VEC) : make_uint4(0, 0, 0, 0);
+
+    float sc[NQ][NU];
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
       const S* e = (const S*)&kr[u];
       float kf[VEC];
 #pragma unroll
@@ -175,158 +170,171 @@ __global__ __launch_bounds__(256) void decode_kernel(Geom g, const typename T::s
         for (int i = 0; i < VEC; ++i) part += qv[r][i] * kf[i];
 #pragma unroll
         for (int off = LPT / 2; off > 0; off >>= 1) part += __shfl_xor(part, off);
-        if (ch == 0 && j < n_tok && r < g.n_q) {
-          const int pj = pos[j];
-          const bool ok = elem_valid(g, r, pj & kIdxMask, (pj >> kPartialBit) & 1);
-          sc[r][j] = ok ? part * g.scale_log2 : kNegInf;
-        }
+        bool ok = pj[u] >= 0 && r < g.n_q;
+        if (ok) ok = elem_valid(g, r, pj[u] & kIdxMask, (pj[u] >> kPartialBit) & 1);
+        sc[r][u] = ok ? part * g.scale_log2 : kNegInf;
       }
     }
-  }
-  __syncthreads();
-
-  // --- split-local softmax -----------------------------------------------------
-  float m_r[NQ], l_r[NQ];
-#pragma unroll
-  for (int r = 0; r < NQ; ++r) {
-    m_r[r] = kNegInf;
-    l_r[r] = 0.f;
-    if (r >= g.n_q) continue;
-    float mx = kNegInf;
-    for (int j = tid; j < n_tok; j += 256) mx = fmaxf(mx, sc[r][j]);
-    mx = block_max(mx, redf);
-    const float mu = mx == kNegInf ? 0.f : mx;
-    float sum = 0.f;
-    for (int j = tid; j < n_tok; j += 256) {
-      const float p = __builtin_amdgcn_exp2f(sc[r][j] - mu);
-      sum += p;
-      sc[r][j] = T::is_f32 ? p : T::to_float(T::from_float(p));   // P -> V dtype
-    }
-    sum = block_sum(sum, redf);
-    m_r[r] = mx;
-    l_r[r] = sum;
-  }
-  __syncthreads();
-
-  // --- P V ---------------------------------------------------------------------
-  float acc[NQ][VEC];
-#pragma unroll
-  for (int r = 0; r < NQ; ++r)
-#pragma unroll
-    for (int i = 0; i < VEC; ++i) acc[r][i] = 0.f;
-  for (int j0 = 0; j0 < n_tok; j0 += TPP * UNR) {
-    uint4 vr[UNR];
-#pragma unroll
-    for (int u = 0; u < UNR; ++u) {
-      const int j = j0 + u * TPP + tk;
-      vr[u] = j < n_tok ? ld_nt16(V + kb + (size_t)(pos[j] & kIdxMask) * D + ch * VEC)
-                        : make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int u = 0; u < UNR; ++u) {
-      const int j = j0 + u * TPP + tk;
-      if (j >= n_tok) continue;
-      const S* e = (const S*)&vr[u];
-#pragma unroll
-      for (int r = 0; r < NQ; ++r) {
-        if (r >= g.n_q) continue;
-        const float p = sc[r][j];
-#pragma unroll
-        for (int i = 0; i < VEC; ++i) acc[r][i] += p * T::to_float(e[i]);
-      }
-    }
-  }
-  // reduce over the token rows of a wave (lanes with equal ch), then over waves
-#pragma unroll
-  for (int r = 0; r < NQ; ++r)
-#pragma unroll
-    for (int i = 0; i < VEC; ++i)
-#pragma unroll
-      for (int off = LPT; off < 64; off <<= 1) acc[r][i] += __shfl_xor(acc[r][i], off);
-  if (lane < LPT) {
-#pragma unroll
-    for (int r = 0; r < NQ; ++r)
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) accbuf[wave][r][ch * VEC + i] = acc[r][i];
-  }
-  __syncthreads();
-  float* out = ws + ((size_t)bh * n_splits + split) * g.n_q * (D + 2);
-  for (int idx = tid; idx < g.n_q * D; idx += 256) {
-    const int r = idx / D, d = idx - r * D;
-    out[(size_t)r * (D + 2) + d] = (accbuf[0][r][d] + accbuf[1][r][d]) + (accbuf[2][r][d] + accbuf[3][r][d]);
-  }
-  if (tid < g.n_q) {
 #pragma unroll
     for (int r = 0; r < NQ; ++r) {
-      if (r == tid) {
-        out[(size_t)r * (D + 2) + D] = m_r[r];
-        out[(size_t)r * (D + 2) + D + 1] = l_r[r];
+      float mx = kNegInf;
+#pragma unroll
+      for (int u = 0; u < NU; ++u) mx = fmaxf(mx, sc[r][u]);
+#pragma unroll
+      for (int off = LPT; off < 64; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+      const float m_new = fmaxf(m[r], mx);
+      const float mu = m_new == kNegInf ? 0.f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m[r] - mu);
+      m[r] = m_new;
+      float rs = 0.f;
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) acc[r][i] *= alpha;
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        const float p = __builtin_amdgcn_exp2f(sc[r][u] - mu);
+        rs += p;
+        const float pv = T::is_f32 ? p : T::to_float(T::from_float(p));   // P -> V dtype
+        const S* e = (const S*)&vr[u];
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) acc[r][i] += pv * T::to_float(e[i]);
+      }
+      l[r] = l[r] * alpha + rs;
+    }
+  }
+  // merge the token-row groups of the wave (same m), then the four waves
+#pragma unroll
+  for (int r = 0; r < NQ; ++r) {
+#pragma unroll
+    for (int off = LPT; off < 64; off <<= 1) {
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) acc[r][i] += __shfl_xor(acc[r][i], off);
+    }
+    // l was accumulated once per token by every lane of its group
+    float lw = l[r];
+#pragma unroll
+    for (int off = LPT; off < 64; off <<= 1) lw += __shfl_xor(lw, off);
+    if (lane < LPT) {
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) wacc[wave][r][ch * VEC + i] = acc[r][i];
+    }
+    if (lane == 0) {
+      wm[wave][r] = m[r];
+      wl[wave][r] = lw;
+    }
+  }
+  __syncthreads();
+  const size_t row_stride = D + 2;
+  float* part = ws + ((size_t)bh * n_splits + split) * g.n_q * row_stride;
+  for (int idx = tid; idx < g.n_q * D; idx += 64 * NW) {
+    const int r = idx / D, d = idx - r * D;
+    float M = kNegInf;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, wm[w][r]);
+    const float Mu = M == kNegInf ? 0.f : M;
+    float L = 0.f, a = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float sw = __builtin_amdgcn_exp2f(wm[w][r] - Mu);
+      L += wl[w][r] * sw;
+      a += wacc[w][r][d] * sw;
+    }
+    if (n_splits == 1) {
+      const bool valid = L > 0.f;
+      O[qb + (size_t)r * D + d] = T::from_float(valid ? a / L : 0.f);
+      if (d == 0) LSE[(size_t)bh * g.n_q + r] = valid ? M * kLn2 + __logf(L) : 0.f;
+    } else {
+      part[r * row_stride + d] = a;
+      if (d == 0) {
+        part[r * row_stride + D] = M;
+        part[r * row_stride + D + 1] = L;
       }
     }
   }
 }
 
+// Merge the n_splits partials of one (b, h, row): one wave per row.
 template <typename T, int D>
-__global__ __launch_bounds__(D) void combine_kernel(const float* __restrict__ ws,
-                                                    typename T::storage* __restrict__ O,
-                                                    float* __restrict__ LSE, int n_q, int n_splits) {
+__global__ __launch_bounds__(64) void combine_kernel(const float* __restrict__ ws,
+                                                     typename T::storage* __restrict__ O,
+                                                     float* __restrict__ LSE, int n_q, int n_splits) {
   const int row = blockIdx.x;
   const int bh = row / n_q, r = row - bh * n_q;
-  const int d = threadIdx.x;
-  const float* base = ws + (size_t)bh * n_splits * n_q * (D + 2) + (size_t)r * (D + 2);
-  const size_t sstride = (size_t)n_q * (D + 2);
+  const int lane = threadIdx.x;
+  const size_t row_stride = D + 2;
+  const float* base = ws + (size_t)bh * n_splits * n_q * row_stride + (size_t)r * row_stride;
+  const size_t sstride = (size_t)n_q * row_stride;
   float M = kNegInf;
   for (int s = 0; s < n_splits; ++s) M = fmaxf(M, base[s * sstride + D]);
   const float Mu = M == kNegInf ? 0.f : M;
-  float L = 0.f, acc = 0.f;
+  float L = 0.f;
+  float a[D / 64];
+#pragma unroll
+  for (int j = 0; j < D / 64; ++j) a[j] = 0.f;
   for (int s = 0; s < n_splits; ++s) {
-    const float w = __builtin_amdgcn_exp2f(base[s * sstride + D] - Mu);
-    L += base[s * sstride + D + 1] * w;
-    acc += base[s * sstride + d] * w;
+    const float* ps = base + s * sstride;
+    const float w = __builtin_amdgcn_exp2f(ps[D] - Mu);
+    L += ps[D + 1] * w;
+#pragma unroll
+    for (int j = 0; j < D / 64; ++j) a[j] += ps[lane + 64 * j] * w;
   }
   const bool valid = L > 0.f;
-  O[(size_t)row * D + d] = T::from_float(valid ? acc / L : 0.f);
-  if (d == 0) LSE[row] = valid ? M * kLn2 + __logf(L) : 0.f;
+#pragma unroll
+  for (int j = 0; j < D / 64; ++j)
+    O[(size_t)row * D + lane + 64 * j] = T::from_float(valid ? a[j] / L : 0.f);
+  if (lane == 0) LSE[row] = valid ? M * kLn2 + __logf(L) : 0.f;
 }
 
 template <typename T, int D, int NQ>
 int launch_decode_t(const Geom& g, const void* q, const void* k, const void* v, void* o, float* lse,
-                    const int32_t* list, int n_ent, float* ws, int n_splits, hipStream_t stream) {
+                    const int32_t* tok, int n_tokens, float* ws, int n_splits, hipStream_t stream) {
   using S = typename T::storage;
   const int BH = g.B * g.H;
-  hipLaunchKernelGGL((decode_kernel<T, D, NQ>), dim3(BH * n_splits), dim3(256), 0, stream, g,
-                     (const S*)q, (const S*)k, (const S*)v, ws, list, n_ent, n_splits);
-  hipLaunchKernelGGL((combine_kernel<T, D>), dim3(BH * g.n_q), dim3(D), 0, stream, ws, (S*)o, lse,
-                     g.n_q, n_splits);
+  hipLaunchKernelGGL((decode_kernel<T, D, NQ>), dim3(BH * n_splits), dim3(64 * kDecodeWaves), 0, stream, g,
+                     (const S*)q, (const S*)k, (const S*)v, (S*)o, lse, ws, tok, n_tokens, n_splits);
+  if (n_splits > 1)
+    hipLaunchKernelGGL((combine_kernel<T, D>), dim3(BH * g.n_q), dim3(64), 0, stream, ws, (S*)o, lse,
+                       g.n_q, n_splits);
   return check_launch("gki_bsa_decode");
 }
 
 template <typename T, int D>
 int launch_decode_d(const Geom& g, const void* q, const void* k, const void* v, void* o, float* lse,
-                    const int32_t* list, int n_ent, float* ws, int n_splits, hipStream_t stream) {
-  if (g.n_q == 1) return launch_decode_t<T, D, 1>(g, q, k, v, o, lse, list, n_ent, ws, n_splits, stream);
-  return launch_decode_t<T, D, kDecodeMaxQ>(g, q, k, v, o, lse, list, n_ent, ws, n_splits, stream);
+                    const int32_t* tok, int n_tokens, float* ws, int n_splits,
+                    hipStream_t stream) {
+  if (g.n_q == 1)
+    return launch_decode_t<T, D, 1>(g, q, k, v, o, lse, tok, n_tokens, ws, n_splits, stream);
+  return launch_decode_t<T, D, kDecodeMaxQ>(g, q, k, v, o, lse, tok, n_tokens, ws, n_splits, stream);
 }
 
 template <typename T>
 int launch_decode(int head_dim, const Geom& g, const void* q, const void* k, const void* v, void* o,
-                  float* lse, const int32_t* list, int n_ent, float* ws, int n_splits,
-                  hipStream_t stream) {
-  if (head_dim == 64) return launch_decode_d<T, 64>(g, q, k, v, o, lse, list, n_ent, ws, n_splits, stream);
-  if (head_dim == 128) return launch_decode_d<T, 128>(g, q, k, v, o, lse, list, n_ent, ws, n_splits, stream);
+                  float* lse, const int32_t* tok, int n_tokens, float* ws,
+                  int n_splits, hipStream_t stream) {
+  if (head_dim == 64)
+    return launch_decode_d<T, 64>(g, q, k, v, o, lse, tok, n_tokens, ws, n_splits, stream);
+  if (head_dim == 128)
+    return launch_decode_d<T, 128>(g, q, k, v, o, lse, tok, n_tokens, ws, n_splits, stream);
   return fail(2, "decode kernel supports head_dim 64 and 128, got " + std::to_string(head_dim));
 }
 
 }  // namespace
 
-int decode_dispatch(int dtype, int head_dim, const Geom& g, const void* q, const void* k, const void* v,
-                    void* o, float* lse, const int32_t* list, int n_ent, float* ws, int n_splits,
-                    hipStream_t stream) {
-  if (dtype == kF32) return launch_decode<F32>(head_dim, g, q, k, v, o, lse, list, n_ent, ws, n_splits, stream);
-  if (dtype == kF16) return launch_decode<F16>(head_dim, g, q, k, v, o, lse, list, n_ent, ws, n_splits, stream);
-  return launch_decode<BF16>(head_dim, g, q, k, v, o, lse, list, n_ent, ws, n_splits, stream);
+int decode_tokens_dispatch(const Geom& g, const int32_t* list, int n_ent, int32_t* tok, int32_t* count,
+                           hipStream_t stream) {
+  hipLaunchKernelGGL(decode_tokens_kernel, dim3(1), dim3(256), 0, stream, g, list, n_ent, tok, count);
+  return check_launch("gki_decode_tokens");
 }
 
-int decode_max_tokens_per_split() { return kMaxTok; }
+int decode_dispatch(int dtype, int head_dim, const Geom& g, const void* q, const void* k, const void* v,
+                    void* o, float* lse, const int32_t* tok, int n_tokens, float* ws,
+                    int n_splits, hipStream_t stream) {
+  if (dtype == kF32)
+    return launch_decode<F32>(head_dim, g, q, k, v, o, lse, tok, n_tokens, ws, n_splits, stream);
+  if (dtype == kF16)
+    return launch_decode<F16>(head_dim, g, q, k, v, o, lse, tok, n_tokens, ws, n_splits, stream);
+  return launch_decode<BF16>(head_dim, g, q, k, v, o, lse, tok, n_tokens, ws, n_splits, stream);
+}
+
+
 
 }  // namespace gki

@@ -23,7 +23,7 @@ _c_float = ctypes.c_float
 SIGNATURES = {
     "gki_abi_version": (ctypes.c_int, []),
     "gki_last_error": (ctypes.c_char_p, []),
-    "gki_tile_sizes": (ctypes.c_int, [_c_ptr] * 5),
+    "gki_tile_sizes": (ctypes.c_int, [_c_ptr] * 4),
     "gki_streaming_mask": (ctypes.c_int, [_c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr]),
     "gki_dense_mask": (ctypes.c_int, [_c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_ptr]),
     "gki_tile_mask": (ctypes.c_int, [_c_ptr, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
@@ -40,6 +40,8 @@ SIGNATURES = {
                                                                    _c_ptr]
                     + [_c_int] * 4 + [_c_float] + [_c_int] * 3 + [_c_ptr]),
     "gki_bsa_decode_workspace_floats": (ctypes.c_int64, [_c_int] * 5),
+    "gki_decode_tokens": (ctypes.c_int, [_c_ptr, _c_int, _c_int, _c_int, _c_ptr] + [_c_int] * 7
+                          + [_c_ptr, _c_ptr, _c_ptr]),
     "gki_bsa_decode": (ctypes.c_int, [_c_ptr] * 5 + [_c_int] * 6 + [_c_ptr, _c_int, _c_ptr]
                        + [_c_int] * 4 + [_c_float] + [_c_int] * 3 + [_c_ptr, _c_int, _c_ptr]),
 }
@@ -91,9 +93,16 @@ def check(rc: int, what: str) -> None:
         raise RuntimeError(f"{what} failed (code {rc}): {msg}")
 
 
+_TILE_SIZES: Optional[dict] = None
+
+
 def tile_sizes() -> dict:
-    lib = load()
-    vals = [ctypes.c_int32() for _ in range(5)]
-    lib.gki_tile_sizes(*[ctypes.byref(v) for v in vals])
-    keys = ("tile_m", "tile_n", "decode_tile_m", "decode_max_q", "decode_max_tokens")
-    return {k: int(v.value) for k, v in zip(keys, vals)}
+    """Kernel tile geometry (queried once from the library)."""
+    global _TILE_SIZES
+    if _TILE_SIZES is None:
+        lib = load()
+        vals = [ctypes.c_int32() for _ in range(4)]
+        lib.gki_tile_sizes(*[ctypes.byref(v) for v in vals])
+        keys = ("tile_m", "tile_n", "decode_tile_m", "decode_max_q")
+        _TILE_SIZES = {k: int(v.value) for k, v in zip(keys, vals)}
+    return dict(_TILE_SIZES)

@@ -55,6 +55,8 @@ class PrefillSchedule:
 class DecodeSchedule:
     tiles: torch.Tensor       # [n_tiles] int32 kept kv tiles of q tile 0
     n_tiles: int
+    tokens: torch.Tensor      # [n_tokens] int32 visible token positions (| partial << 30)
+    n_tokens: int
 
 
 def _stream(device: torch.device) -> int:
@@ -162,15 +164,26 @@ def prefill_schedule(mask: torch.Tensor, n_q: int, n_kv: int, block_m: int,
     return _CACHE.get(mask, ("prefill", n_q, n_kv, block_m, block_n, tm, tn), build)
 
 
-def decode_schedule(mask: torch.Tensor, n_q: int, n_kv: int, block_m: int,
-                    block_n: int) -> DecodeSchedule:
-    """Kept kv tiles (64 keys each) of the single decode q tile (n_q rows)."""
+def decode_schedule(mask: torch.Tensor, n_q: int, n_kv: int, block_m: int, block_n: int,
+                    is_causal: bool, sink: int, window: int) -> DecodeSchedule:
+    """Kept kv tiles (64 keys each) of the single decode q tile (n_q rows) and
+    the token-exact stream of positions the decode kernel reads."""
     ts = _lib.tile_sizes()
     tm, tn = ts["decode_tile_m"], ts["tile_n"]
 
     def build() -> DecodeSchedule:
+        lib = _lib.load()
         tiles = _tile_matrix(mask, n_q, n_kv, block_m, block_n, tm, tn)
         lists = _lists_of(tiles)
-        return DecodeSchedule(lists.row_idx, lists.nnz)
+        tokens = torch.empty(max(lists.nnz * tn, 1), dtype=torch.int32, device=mask.device)
+        count = torch.zeros(1, dtype=torch.int32, device=mask.device)
+        n_qb, n_kb = (int(s) for s in mask.shape)
+        _lib.check(lib.gki_decode_tokens(lists.row_idx.data_ptr(), lists.nnz, n_q, n_kv,
+                                         mask.data_ptr(), n_qb, n_kb, block_m, block_n,
+                                         int(bool(is_causal)), sink, window, tokens.data_ptr(),
+                                         count.data_ptr(), _stream(mask.device)), "gki_decode_tokens")
+        n_tokens = int(count.item())
+        return DecodeSchedule(lists.row_idx, lists.nnz, tokens[:n_tokens], n_tokens)
 
-    return _CACHE.get(mask, ("decode", n_q, n_kv, block_m, block_n, tm, tn), build)
+    key = ("decode", n_q, n_kv, block_m, block_n, tm, tn, bool(is_causal), sink, window)
+    return _CACHE.get(mask, key, build)

@@ -26,8 +26,8 @@ from .lists import _CACHE, decode_schedule, prefill_schedule
 _DTYPE_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 _HEAD_DIMS = (16, 32, 64, 128)
 _DECODE_HEAD_DIMS = (64, 128)
-# total decode workgroups to aim for (256 CUs x 16 resident 256-thread groups)
-_DECODE_TARGET_WGS = 4096
+# decode workgroups to aim for: one 1024-thread group on each of the 256 CUs
+_DECODE_TARGET_WGS = 256
 
 
 def _device_mask(block_mask: torch.Tensor, device: torch.device) -> torch.Tensor:
@@ -40,12 +40,12 @@ def _device_mask(block_mask: torch.Tensor, device: torch.device) -> torch.Tensor
     return block_mask.to(device=device, dtype=torch.int32).contiguous()
 
 
-def _decode_splits(n_tiles: int, bh: int, tile_n: int, max_tokens: int) -> int:
-    est = max(n_tiles, 1) * tile_n
-    need = -(-est // max_tokens)              # at most max_tokens tokens per split
-    want = -(-_DECODE_TARGET_WGS // bh)       # fill the machine
-    cap = max(1, est // tile_n)               # at least one tile of tokens per split
-    return max(need, min(want, cap))
+def _decode_splits(n_tokens: int, bh: int) -> int:
+    """1024-thread workgroups per (b, h) for the decode step: about one per CU
+    in total, but at least ~1024 tokens (64 per wave) per workgroup."""
+    want = -(-_DECODE_TARGET_WGS // bh)
+    cap = max(1, n_tokens // 1024)
+    return max(1, min(want, cap))
 
 
 class _BlockSparseFlashAttention(torch.autograd.Function):
@@ -107,14 +107,18 @@ class _BlockSparseFlashAttention(torch.autograd.Function):
             stream = torch.cuda.current_stream(dev).cuda_stream
             ts = _lib.tile_sizes()
             if N_Q <= ts["decode_max_q"] and D in _DECODE_HEAD_DIMS:
-                sched = decode_schedule(block_mask, N_Q, N_KV, block_m, block_n)
-                n_splits = _decode_splits(sched.n_tiles, B * H, ts["tile_n"], ts["decode_max_tokens"])
-                ws = torch.empty(int(lib.gki_bsa_decode_workspace_floats(B, H, N_Q, D, n_splits)),
-                                 dtype=torch.float32, device=dev)
+                sched = decode_schedule(block_mask, N_Q, N_KV, block_m, block_n, bool(is_causal),
+                                        int(sink_size), int(window_size))
+                n_splits = _decode_splits(sched.n_tokens, B * H)
+                ws_ptr = 0
+                if n_splits > 1:
+                    ws = torch.empty(int(lib.gki_bsa_decode_workspace_floats(B, H, N_Q, D, n_splits)),
+                                     dtype=torch.float32, device=dev)
+                    ws_ptr = ws.data_ptr()
                 _lib.check(lib.gki_bsa_decode(
                     q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), dtype,
-                    B, H, N_Q, N_KV, D, sched.tiles.data_ptr(), sched.n_tiles, *common,
-                    ws.data_ptr(), n_splits, stream), "gki_bsa_decode")
+                    B, H, N_Q, N_KV, D, sched.tokens.data_ptr(), sched.n_tokens, *common,
+                    ws_ptr, n_splits, stream), "gki_bsa_decode")
             else:
                 sched = prefill_schedule(block_mask, N_Q, N_KV, block_m, block_n)
                 _lib.check(lib.gki_bsa_fwd(

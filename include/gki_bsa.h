@@ -34,10 +34,10 @@ int gki_abi_version(void);
 const char* gki_last_error(void);
 
 /* Kernel tile geometry the schedules must be built for: prefill/backward tile
- * (tile_m x tile_n), decode q tile rows, max query rows handled by the decode
- * kernel, and max tokens one decode split holds. Any pointer may be NULL. */
+ * (tile_m x tile_n), decode q tile rows, and max query rows handled by the
+ * decode kernel. Any pointer may be NULL. */
 int gki_tile_sizes(int32_t* tile_m, int32_t* tile_n, int32_t* decode_tile_m,
-                   int32_t* decode_max_q, int32_t* decode_max_tokens);
+                   int32_t* decode_max_q);
 
 /* Block-level StreamingLLM mask, bit-exact with `make_streaming_mask`
  * (sparse_triton_kernel.py:104-181): keep (i, j) iff q_hi > k_lo and
@@ -105,18 +105,32 @@ int gki_bsa_bwd(const void* q, const void* k, const void* v, const void* o,
                 int32_t block_m, int32_t block_n, float softmax_scale, int32_t is_causal,
                 int32_t sink_size, int32_t window_size, void* stream);
 
-/* Floats of workspace gki_bsa_decode needs for a given split count. */
+/* Floats of workspace gki_bsa_decode needs for a given split count (none is
+ * read when n_splits == 1). */
 int64_t gki_bsa_decode_workspace_floats(int32_t B, int32_t H, int32_t n_q,
                                         int32_t head_dim, int32_t n_splits);
 
+/* Decode token stream (once per mask): expands the kept kv tiles of the single
+ * decode q tile (`tile_list`, n_tiles entries of the decode_tile_m x tile_n
+ * schedule) into the positions of the tokens some query row can see (the hull
+ * of each tile's sink prefix / window suffix / in-bounds rows), entry =
+ * position | partial << 30. `tokens` holds n_tiles * tile_n int32; the count
+ * is written to the device scalar `n_tokens`. No reference counterpart: the
+ * reference visits whole tiles (sparse_triton_kernel.py:283-299). */
+int gki_decode_tokens(const int32_t* tile_list, int32_t n_tiles, int32_t n_q, int32_t n_kv,
+                      const int32_t* mask, int32_t n_qb, int32_t n_kb, int32_t block_m,
+                      int32_t block_n, int32_t is_causal, int32_t sink_size,
+                      int32_t window_size, int32_t* tokens, int32_t* n_tokens, void* stream);
+
 /* Decode step (n_q <= decode_max_q, head_dim 64 or 128): replaces the
  * reference's BLOCK_M = 1 use of `_fwd_kernel` for decode
- * (benchmark.py:500-511, 802-804) with a split-KV pass over the kept kv tiles
- * of the single decode q tile (`tile_list`, n_tiles entries) and a combine.
- * Same outputs as gki_bsa_fwd. n_tiles * tile_n <= n_splits * decode_max_tokens. */
+ * (benchmark.py:500-511, 802-804). n_splits workgroups per (b, h) each stream
+ * an equal slice of the token list (from gki_decode_tokens); with
+ * n_splits == 1 they write O / LSE directly, otherwise they write partials to
+ * `workspace` and a second launch merges them. Same outputs as gki_bsa_fwd. */
 int gki_bsa_decode(const void* q, const void* k, const void* v, void* o, float* lse,
                    int32_t dtype, int32_t B, int32_t H, int32_t n_q, int32_t n_kv,
-                   int32_t head_dim, const int32_t* tile_list, int32_t n_tiles,
+                   int32_t head_dim, const int32_t* tokens, int32_t n_tokens,
                    const int32_t* mask, int32_t n_qb, int32_t n_kb, int32_t block_m,
                    int32_t block_n, float softmax_scale, int32_t is_causal,
                    int32_t sink_size, int32_t window_size, float* workspace,

@@ -116,9 +116,13 @@ def test_prefill_schedule_matches_oracle(n_q, n_kv, sink, window, bm, bn):
 
 def test_decode_schedule_matches_oracle():
     m = so.block_mask(1, 100000, 4, 2048, 1, 64)
-    sched = decode_schedule(torch.from_numpy(m).to(DEV), 1, 100000, 1, 64)
+    sched = decode_schedule(torch.from_numpy(m).to(DEV), 1, 100000, 1, 64, True, 4, 2048)
     assert sched.n_tiles == 34
     np.testing.assert_array_equal(sched.tiles.cpu().numpy(), [0] + list(range(1530, 1563)))
+    # token-exact stream: the 4 sink tokens and the 2048-token window
+    assert sched.n_tokens == 4 + 2048
+    np.testing.assert_array_equal(sched.tokens.cpu().numpy(),
+                                  list(range(4)) + list(range(100000 - 2048, 100000)))
 
 
 # ---------------------------------------------------------------------------

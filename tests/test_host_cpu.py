@@ -99,8 +99,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_tile_sizes():
     ts = _lib.tile_sizes()
-    assert ts == {"tile_m": 64, "tile_n": 64, "decode_tile_m": 16, "decode_max_q": 4,
-                  "decode_max_tokens": 512}
+    assert ts == {"tile_m": 64, "tile_n": 64, "decode_tile_m": 16, "decode_max_q": 4}
 
 
 def test_capi_rejects_bad_arguments_before_launch():
@@ -131,3 +130,7 @@ def test_capi_rejects_bad_arguments_before_launch():
     assert lib.gki_dense_mask(1, 60, 64, 16, 16, 0, null) == 1
     assert b"divide" in lib.gki_last_error()
     assert lib.gki_bsa_decode_workspace_floats(2, 3, 1, 128, 5) == 2 * 3 * 5 * 130
+    # decode: several splits need a workspace
+    rc = lib.gki_bsa_decode(1, 1, 1, 1, 1, 2, 1, 1, 1, 1000, 64, 1, 300, 1, 1, 16, 1, 64, 0.1, 1, 4,
+                            8, 0, 2, null)
+    assert rc == 1 and b"workspace" in lib.gki_last_error()
