@@ -56,65 +56,6 @@ __global__ __launch_bounds__(256) void delta_kernel(const typename T::storage* _
   if (row < rows && ch == 0) delta[row] = acc;
 }
 
-// ---------------------------------------------------------------------------
-// Shared staging: a 64-row tile of a [n, D] 16-bit matrix into LDS, both
-// row-major (stride D+8) and transposed (XOR-swizzled 8-element chunks), from a
-// register prefetch. Task (rg, ch) covers rows 4rg..4rg+3, columns 8ch..8ch+7.
-// ---------------------------------------------------------------------------
-template <int D>
-struct Stage16 {
-  static constexpr int LD = D + 8;
-  static constexpr int CPR = D / 8;
-  static constexpr int TASKS = 16 * CPR;
-  static constexpr int P = (TASKS + 255) / 256;
-  uint4 reg[P][4];
-
-  __device__ inline void load(const uint16_t* base, int r0, int n_rows, int tid) {
-#pragma unroll
-    for (int p = 0; p < P; ++p) {
-      const int task = tid + 256 * p;
-      const int rg = task & 15, ch = task >> 4;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = r0 + 4 * rg + r;
-        reg[p][r] = (task < TASKS && row < n_rows) ? *(const uint4*)(base + (size_t)row * D + ch * 8)
-                                                   : make_uint4(0, 0, 0, 0);
-      }
-    }
-  }
-  __device__ inline void store(uint16_t* rowmajor, uint16_t* transposed, int tid) const {
-#pragma unroll
-    for (int p = 0; p < P; ++p) {
-      const int task = tid + 256 * p;
-      if (task >= TASKS) continue;
-      const int rg = task & 15, ch = task >> 4;
-      if (rowmajor) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) *(uint4*)(&rowmajor[(4 * rg + r) * LD + ch * 8]) = reg[p][r];
-      }
-      if (transposed) {
-        const uint16_t* e0 = (const uint16_t*)&reg[p][0];
-        const uint16_t* e1 = (const uint16_t*)&reg[p][1];
-        const uint16_t* e2 = (const uint16_t*)&reg[p][2];
-        const uint16_t* e3 = (const uint16_t*)&reg[p][3];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int d = ch * 8 + j;
-          const int phys = (((rg >> 1) ^ (d & 7)) << 3) + ((rg & 1) << 2);
-          uint2 w;
-          w.x = (uint32_t)e0[j] | ((uint32_t)e1[j] << 16);
-          w.y = (uint32_t)e2[j] | ((uint32_t)e3[j] << 16);
-          *(uint2*)(&transposed[d * 64 + phys]) = w;
-        }
-      }
-    }
-  }
-};
-// Read the 8 contiguous elements [c8*8, c8*8+8) of transposed row d.
-__device__ inline uint4 ldsT(const uint16_t* transposed, int d, int c8) {
-  return *(const uint4*)(&transposed[d * 64 + ((c8 ^ (d & 7)) << 3)]);
-}
-
 template <int D>
 struct Stage32 {
   static constexpr int LD = D + 4;
@@ -161,18 +102,9 @@ __device__ inline void dkdv_tile_of(int b, int BH, int n_kt, int n_heavy, const 
 }
 
 // ---------------------------------------------------------------------------
-// dK / dV, 16-bit
+// dK / dV, 16-bit. Q and dO tiles row-major in LDS (double-buffered); the
+// dV += P^T dO and dK += dS^T Q operands dO / Q come from lds_tr8.
 // ---------------------------------------------------------------------------
-template <int D>
-struct DkdvSmem16 {
-  uint16_t q[64 * (D + 8)];
-  uint16_t qt[D * 64];
-  uint16_t dout[64 * (D + 8)];
-  uint16_t dot[D * 64];
-  float lse2[64];
-  float dlt[64];
-};
-
 template <typename T, int D>
 __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
     Geom g, const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
@@ -182,9 +114,12 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
     const int32_t* __restrict__ order, int n_heavy, int n_kt) {
   constexpr int KS = (D + 31) / 32;
   constexpr int DT = D / 16;
-  constexpr int LD = D + 8;
-  __shared__ DkdvSmem16<D> sm;
-  Stage16<D> sq, sdo;
+  using Tile = RowTile<D>;
+  constexpr int LD = Tile::LD;
+  __shared__ __align__(16) uint16_t sq[2][64 * LD];
+  __shared__ __align__(16) uint16_t sdo[2][64 * LD];
+  __shared__ __align__(16) float slse[2][64];
+  __shared__ __align__(16) float sdlt[2][64];
 
   const int BH = g.B * g.H;
   int bh, kt;
@@ -209,36 +144,46 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
   for (int i = 0; i < DT; ++i) dk[i] = dv[i] = floatx4{0.f, 0.f, 0.f, 0.f};
 
   const int e_beg = col_ptr[kt], e_end = col_ptr[kt + 1];
+  Tile tq, tdo;
   float lreg = 0.f, dreg = 0.f;
   auto load_tile = [&](int q0) {
-    sq.load(Q + qb, q0, g.n_q, tid);
-    sdo.load(dO + qb, q0, g.n_q, tid);
+    tq.load(Q + qb, q0, g.n_q, tid);
+    tdo.load(dO + qb, q0, g.n_q, tid);
     if (tid < 64) {
       const int r = q0 + tid;
       lreg = r < g.n_q ? LSE[(size_t)bh * g.n_q + r] * kLog2e : 0.f;
       dreg = r < g.n_q ? Delta[(size_t)bh * g.n_q + r] : 0.f;
     }
   };
-  if (e_beg < e_end) load_tile((col_idx[e_beg] & kIdxMask) * kTileM);
+  auto store_tile = [&](int buf) {
+    tq.store(sq[buf], tid);
+    tdo.store(sdo[buf], tid);
+    if (tid < 64) {
+      slse[buf][tid] = lreg;
+      sdlt[buf][tid] = dreg;
+    }
+  };
+  if (e_beg < e_end) {
+    load_tile((col_idx[e_beg] & kIdxMask) * kTileM);
+    store_tile(0);
+  }
+  __syncthreads();
 
   const int kv_hi_wave = min(k_w + 15, g.n_kv - 1);
   for (int e = e_beg; e < e_end; ++e) {
+    const int buf = (e - e_beg) & 1;
     const int ent = col_idx[e];
     const int q0 = (ent & kIdxMask) * kTileM;
     const bool partial = (ent >> kPartialBit) & 1;
-    __syncthreads();
-    sq.store(sm.q, sm.qt, tid);
-    sdo.store(sm.dout, sm.dot, tid);
-    if (tid < 64) {
-      sm.lse2[tid] = lreg;
-      sm.dlt[tid] = dreg;
-    }
-    __syncthreads();
-    if (e + 1 < e_end) load_tile((col_idx[e + 1] & kIdxMask) * kTileM);
+    const bool has_next = e + 1 < e_end;
+    if (has_next) load_tile((col_idx[e + 1] & kIdxMask) * kTileM);
+    const uint16_t* cq = sq[buf];
+    const uint16_t* cdo = sdo[buf];
 
     const bool need_mask = partial || (q0 + kTileM > g.n_q) || (k_w + 15 >= g.n_kv) ||
                            !tile_all_visible(g, q0, min(q0 + kTileM - 1, g.n_q - 1), k_w, kv_hi_wave);
-    // S and dP for the four 16-row q subtiles (rows rho(t, .)).
+    // S and dP for the four 16-row q subtiles (rows rho(t, .)); accumulator
+    // element i of lane (grp, col) is q row rho(t, 4 grp + i), kv row my_kv
     floatx4 p[4], ds[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
@@ -248,35 +193,36 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         const int d0 = 32 * ks + 8 * grp;
-        const uint4 aq = (d0 < D) ? *(const uint4*)(&sm.q[r * LD + d0]) : make_uint4(0, 0, 0, 0);
-        const uint4 ad = (d0 < D) ? *(const uint4*)(&sm.dout[r * LD + d0]) : make_uint4(0, 0, 0, 0);
+        const uint4 aq = (d0 < D) ? *(const uint4*)(&cq[r * LD + d0]) : make_uint4(0, 0, 0, 0);
+        const uint4 ad = (d0 < D) ? *(const uint4*)(&cdo[r * LD + d0]) : make_uint4(0, 0, 0, 0);
         s = T::mfma(aq, kf[ks], s);
         dp = T::mfma(ad, vf[ks], dp);
       }
+      const int qr0 = rho(t, 4 * grp);
+      const float4 lse4 = *(const float4*)(&slse[buf][qr0]);
+      const float4 dlt4 = *(const float4*)(&sdlt[buf][qr0]);
+      const float lv[4] = {lse4.x, lse4.y, lse4.z, lse4.w};
+      const float dv4[4] = {dlt4.x, dlt4.y, dlt4.z, dlt4.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int qr = rho(t, 4 * grp + i);
-        float pv = __builtin_amdgcn_exp2f(s[i] * g.scale_log2 - sm.lse2[qr]);
-        if (need_mask && !elem_valid(g, q0 + qr, my_kv, partial)) pv = 0.f;
+        float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], g.scale_log2, -lv[i]));
+        if (need_mask && !elem_valid(g, q0 + qr0 + i, my_kv, partial)) pv = 0.f;
         p[t][i] = pv;
-        ds[t][i] = pv * (dp[i] - sm.dlt[qr]) * g.scale;
+        ds[t][i] = pv * (dp[i] - dv4[i]) * g.scale;
       }
     }
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
-      float pa[8] = {p[2 * st][0], p[2 * st][1], p[2 * st][2], p[2 * st][3],
-                     p[2 * st + 1][0], p[2 * st + 1][1], p[2 * st + 1][2], p[2 * st + 1][3]};
-      float da[8] = {ds[2 * st][0], ds[2 * st][1], ds[2 * st][2], ds[2 * st][3],
-                     ds[2 * st + 1][0], ds[2 * st + 1][1], ds[2 * st + 1][2], ds[2 * st + 1][3]};
-      const uint4 ap = pack8<T>(pa);
-      const uint4 ad = pack8<T>(da);
+      const uint4 ap = pack8<T>(p[2 * st], p[2 * st + 1]);
+      const uint4 ad = pack8<T>(ds[2 * st], ds[2 * st + 1]);
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        const int d = 16 * dt + col;
-        dv[dt] = T::mfma(ap, ldsT(sm.dot, d, 4 * st + grp), dv[dt]);
-        dk[dt] = T::mfma(ad, ldsT(sm.qt, d, 4 * st + grp), dk[dt]);
+        dv[dt] = T::mfma(ap, lds_tr8(cdo, LD, 32 * st, 16 * dt, lane), dv[dt]);
+        dk[dt] = T::mfma(ad, lds_tr8(cq, LD, 32 * st, 16 * dt, lane), dk[dt]);
       }
     }
+    if (has_next) store_tile(buf ^ 1);
+    __syncthreads();
   }
 
   // dK/dV accumulators: lane holds rows k_w + 4grp + i, column 16dt + col.
@@ -314,7 +260,7 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_32(
   constexpr int KS = D / 4;
   constexpr int DT = D / 16;
   constexpr int LD = D + 4;
-  __shared__ DkdvSmem32<D> sm;
+  __shared__ __align__(16) DkdvSmem32<D> sm;
   Stage32<D> sq, sdo;
 
   const int BH = g.B * g.H;
@@ -406,15 +352,9 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_32(
 }
 
 // ---------------------------------------------------------------------------
-// dQ, 16-bit
+// dQ, 16-bit. K and V tiles row-major in LDS (double-buffered); the
+// dQ^T += K^T dS^T operand K^T comes from lds_tr8.
 // ---------------------------------------------------------------------------
-template <int D>
-struct DqSmem16 {
-  uint16_t k[64 * (D + 8)];
-  uint16_t kt[D * 64];
-  uint16_t v[64 * (D + 8)];
-};
-
 template <typename T, int D>
 __global__ __launch_bounds__(256, 2) void dq_kernel_16(
     Geom g, const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
@@ -423,9 +363,10 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_16(
     const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ row_idx, int n_qt) {
   constexpr int KS = (D + 31) / 32;
   constexpr int DT = D / 16;
-  constexpr int LD = D + 8;
-  __shared__ DqSmem16<D> sm;
-  Stage16<D> sk, sv;
+  using Tile = RowTile<D>;
+  constexpr int LD = Tile::LD;
+  __shared__ __align__(16) uint16_t sk[2][64 * LD];
+  __shared__ __align__(16) uint16_t sv[2][64 * LD];
 
   const int n_wg = n_qt * g.B * g.H;
   const int wg = xcd_remap(blockIdx.x, n_wg);
@@ -453,25 +394,29 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_16(
   for (int i = 0; i < DT; ++i) dq[i] = floatx4{0.f, 0.f, 0.f, 0.f};
 
   const int e_beg = row_ptr[qt], e_end = row_ptr[qt + 1];
+  Tile tk, tv;
   if (e_beg < e_end) {
     const int k0 = (row_idx[e_beg] & kIdxMask) * kTileN;
-    sk.load(K + kb, k0, g.n_kv, tid);
-    sv.load(V + kb, k0, g.n_kv, tid);
+    tk.load(K + kb, k0, g.n_kv, tid);
+    tv.load(V + kb, k0, g.n_kv, tid);
+    tk.store(sk[0], tid);
+    tv.store(sv[0], tid);
   }
+  __syncthreads();
   const int q_hi_wave = min(q0 + 15, g.n_q - 1);
   for (int e = e_beg; e < e_end; ++e) {
+    const int buf = (e - e_beg) & 1;
     const int ent = row_idx[e];
     const int k0 = (ent & kIdxMask) * kTileN;
     const bool partial = (ent >> kPartialBit) & 1;
-    __syncthreads();
-    sk.store(sm.k, sm.kt, tid);
-    sv.store(sm.v, nullptr, tid);
-    __syncthreads();
-    if (e + 1 < e_end) {
+    const bool has_next = e + 1 < e_end;
+    if (has_next) {
       const int k1 = (row_idx[e + 1] & kIdxMask) * kTileN;
-      sk.load(K + kb, k1, g.n_kv, tid);
-      sv.load(V + kb, k1, g.n_kv, tid);
+      tk.load(K + kb, k1, g.n_kv, tid);
+      tv.load(V + kb, k1, g.n_kv, tid);
     }
+    const uint16_t* ck = sk[buf];
+    const uint16_t* cv = sv[buf];
     const bool need_mask = partial || (q0 + 15 >= g.n_q) || (k0 + kTileN > g.n_kv) ||
                            !tile_all_visible(g, q0, q_hi_wave, k0, k0 + kTileN - 1);
     floatx4 ds[4];
@@ -483,33 +428,36 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_16(
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         const int d0 = 32 * ks + 8 * grp;
-        const uint4 ak = (d0 < D) ? *(const uint4*)(&sm.k[r * LD + d0]) : make_uint4(0, 0, 0, 0);
-        const uint4 av = (d0 < D) ? *(const uint4*)(&sm.v[r * LD + d0]) : make_uint4(0, 0, 0, 0);
+        const uint4 ak = (d0 < D) ? *(const uint4*)(&ck[r * LD + d0]) : make_uint4(0, 0, 0, 0);
+        const uint4 av = (d0 < D) ? *(const uint4*)(&cv[r * LD + d0]) : make_uint4(0, 0, 0, 0);
         s = T::mfma(ak, qf[ks], s);
         dp = T::mfma(av, df[ks], dp);
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float pv = __builtin_amdgcn_exp2f(s[i] * g.scale_log2 - lse2);
+        float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], g.scale_log2, -lse2));
         if (need_mask && !elem_valid(g, my_q, k0 + rho(t, 4 * grp + i), partial)) pv = 0.f;
         ds[t][i] = pv * (dp[i] - dlt) * g.scale;
       }
     }
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
-      float da[8] = {ds[2 * st][0], ds[2 * st][1], ds[2 * st][2], ds[2 * st][3],
-                     ds[2 * st + 1][0], ds[2 * st + 1][1], ds[2 * st + 1][2], ds[2 * st + 1][3]};
-      const uint4 b = pack8<T>(da);
+      const uint4 b = pack8<T>(ds[2 * st], ds[2 * st + 1]);
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) dq[dt] = T::mfma(ldsT(sm.kt, 16 * dt + col, 4 * st + grp), b, dq[dt]);
+      for (int dt = 0; dt < DT; ++dt) dq[dt] = T::mfma(lds_tr8(ck, LD, 32 * st, 16 * dt, lane), b, dq[dt]);
     }
+    if (has_next) {
+      tk.store(sk[buf ^ 1], tid);
+      tv.store(sv[buf ^ 1], tid);
+    }
+    __syncthreads();
   }
   if (my_q < g.n_q) {
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
       uint2 w;
-      w.x = (uint32_t)T::from_float(dq[dt][0]) | ((uint32_t)T::from_float(dq[dt][1]) << 16);
-      w.y = (uint32_t)T::from_float(dq[dt][2]) | ((uint32_t)T::from_float(dq[dt][3]) << 16);
+      w.x = pack2<T>(dq[dt][0], dq[dt][1]);
+      w.y = pack2<T>(dq[dt][2], dq[dt][3]);
       *(uint2*)(dQ + qb + (size_t)my_q * D + 16 * dt + 4 * grp) = w;
     }
   }
@@ -533,7 +481,7 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_32(
   constexpr int KS = D / 4;
   constexpr int DT = D / 16;
   constexpr int LD = D + 4;
-  __shared__ DqSmem32<D> sm;
+  __shared__ __align__(16) DqSmem32<D> sm;
   Stage32<D> sk, sv;
 
   const int n_wg = n_qt * g.B * g.H;

@@ -54,6 +54,7 @@ int make_geom(Geom& g, int dtype, int B, int H, int n_q, int n_kv, int head_dim,
   GKI_REQUIRE(n_qb == (n_q + block_m - 1) / block_m && n_kb == (n_kv + block_n - 1) / block_n, 1,
               "block mask shape does not match ceil(n_q/block_m) x ceil(n_kv/block_n)");
   GKI_REQUIRE(sink >= 0 && window >= 0, 1, "sink_size and window_size must be non-negative");
+  GKI_REQUIRE(scale > 0.f && scale < __builtin_huge_valf(), 1, "softmax_scale must be positive and finite");
   GKI_REQUIRE((int64_t)n_kv < (1ll << kPartialBit), 1, "n_kv too large");
   GKI_REQUIRE(mask != nullptr, 1, "null block mask");
   g.B = B;

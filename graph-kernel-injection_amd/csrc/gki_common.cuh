@@ -70,16 +70,80 @@ __device__ inline uint4 ld_nt16(const void* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// Two fp32 -> two 16-bit elements in one v_cvt_pk_{bf16,f16}_f32 (RNE).
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+template <typename T>
+__device__ inline uint32_t pack2(float a, float b);
+template <>
+__device__ inline uint32_t pack2<BF16>(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+}
+template <>
+__device__ inline uint32_t pack2<F16>(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, f16x2));
+}
+
 // Pack 8 fp32 values into 8 16-bit elements (one 16x16x32 MFMA operand).
 template <typename T>
 __device__ inline uint4 pack8(const float* v) {
-  uint4 r;
-  r.x = (uint32_t)T::from_float(v[0]) | ((uint32_t)T::from_float(v[1]) << 16);
-  r.y = (uint32_t)T::from_float(v[2]) | ((uint32_t)T::from_float(v[3]) << 16);
-  r.z = (uint32_t)T::from_float(v[4]) | ((uint32_t)T::from_float(v[5]) << 16);
-  r.w = (uint32_t)T::from_float(v[6]) | ((uint32_t)T::from_float(v[7]) << 16);
-  return r;
+  return make_uint4(pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]), pack2<T>(v[4], v[5]),
+                    pack2<T>(v[6], v[7]));
 }
+// Same, from the accumulators of two 16x16 subtiles (rows 0-3 then 4-7).
+template <typename T>
+__device__ inline uint4 pack8(const floatx4& lo, const floatx4& hi) {
+  return make_uint4(pack2<T>(lo[0], lo[1]), pack2<T>(lo[2], lo[3]), pack2<T>(hi[0], hi[1]),
+                    pack2<T>(hi[2], hi[3]));
+}
+
+// Transposed MFMA operand from a row-major 16-bit LDS tile with `ld` elements
+// per row, via ds_read_b64_tr_b16: within each 16-lane group, lane l points at
+// row k0 + l/4, columns n0 + 4*(l%4) .. +3, and the instruction hands lane i
+// column n0 + i of those four rows. Two reads give lane (g, c) = (lane/16,
+// lane%16) the 8 elements tile[k0 + 8g + e][n0 + c], e = 0..7: the K-operand
+// layout of v_mfma_f32_16x16x32_{bf16,f16} for a matrix stored K-major.
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+__device__ inline uint4 lds_tr8(const uint16_t* tile, int ld, int k0, int n0, int lane) {
+  const int g = lane >> 4, l = lane & 15;
+  const uint16_t* p = tile + (k0 + 8 * g + (l >> 2)) * ld + n0 + 4 * (l & 3);
+  const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)p);
+  const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(p + 4 * ld));
+  const uint2 a = __builtin_bit_cast(uint2, lo), b = __builtin_bit_cast(uint2, hi);
+  return make_uint4(a.x, a.y, b.x, b.y);
+}
+
+// Stage a 64-row tile of a row-major [n, D] 16-bit matrix: each thread moves
+// P 16-byte chunks, consecutive threads covering consecutive bytes of a row.
+template <int D>
+struct RowTile {
+  static constexpr int LD = D + 8;           // padded LDS row (elements)
+  static constexpr int CPR = D / 8;          // 16-byte chunks per row
+  static constexpr int CH = 64 * CPR;
+  static constexpr int P = (CH + 255) / 256;
+  uint4 reg[P];
+  __device__ inline void load(const uint16_t* base, int r0, int n_rows, int tid) {
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int c = tid + 256 * p;
+      const int r = c / CPR, ch = c - r * CPR;
+      reg[p] = (c < CH && r0 + r < n_rows) ? *(const uint4*)(base + (size_t)(r0 + r) * D + ch * 8)
+                                           : make_uint4(0, 0, 0, 0);
+    }
+  }
+  __device__ inline void store(uint16_t* lds, int tid) const {
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int c = tid + 256 * p;
+      if (c < CH) {
+        const int r = c / CPR, ch = c - r * CPR;
+        *(uint4*)(&lds[r * LD + ch * 8]) = reg[p];
+      }
+    }
+  }
+};
 
 // ---------------------------------------------------------------------------
 // Kernel tiling. All prefill / backward kernels use 64x64 (q x kv) tiles, four

@@ -13,24 +13,16 @@
 //    max / sum are per-lane scalars; row reductions need two cross-group shuffles.
 //  * K tile rows are fetched through the rho() permutation, which makes the S^T
 //    accumulators of subtiles (2s, 2s+1) the B operand of O^T += V^T P^T as-is.
-//  * K (row-major) and V^T (XOR-swizzled) tiles are staged in LDS; the next
-//    tile's global loads are issued before the current tile's MFMAs.
+//  * K and V tiles are staged row-major in LDS with coalesced 16-byte loads,
+//    double-buffered (one barrier per tile; the next tile's global loads are in
+//    flight during the current tile's MFMAs). V^T operands are read with the
+//    gfx950 LDS transpose read (ds_read_b64_tr_b16).
+//  * The O^T rescale is skipped, exactly, when no row max of the wave moved.
 //  * Only kept tiles are visited: the workgroup walks a GPU-resident CSR list.
 #include "gki_common.cuh"
 
 namespace gki {
 namespace {
-
-template <typename T, int D>
-struct FwdCfg;
-
-// 16-bit element types: K row-major (padded), V transposed.
-template <int D, typename T>
-struct FwdSmem16 {
-  static constexpr int KLD = D + 8;
-  uint16_t k[kTileN * KLD];
-  uint16_t vt[D * kTileN];
-};
 
 template <int D>
 struct FwdSmem32 {
@@ -40,7 +32,8 @@ struct FwdSmem32 {
 };
 
 // ---------------------------------------------------------------------------
-// 16-bit path
+// 16-bit path: K and V tiles row-major in LDS (double-buffered, one barrier per
+// tile); V^T operands come from ds_read_b64_tr_b16 (lds_tr8).
 // ---------------------------------------------------------------------------
 template <typename T, int D>
 __global__ __launch_bounds__(256, 2) void fwd_kernel_16(
@@ -49,13 +42,10 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel_16(
     const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ row_idx, int n_qt) {
   constexpr int KS = (D + 31) / 32;   // k-steps of the QK^T contraction
   constexpr int DT = D / 16;          // 16-row tiles of O^T
-  constexpr int CPR = D / 8;          // 16-byte chunks per row
-  constexpr int KCH = kTileN * CPR;   // chunks in a K tile
-  constexpr int KP = (KCH + 255) / 256;
-  constexpr int VTASK = 16 * CPR;     // (4-row group, chunk) tasks for V^T staging
-  constexpr int VP = (VTASK + 255) / 256;
-  using Smem = FwdSmem16<D, T>;
-  __shared__ Smem sm;
+  using Tile = RowTile<D>;
+  constexpr int LD = Tile::LD;
+  __shared__ __align__(16) uint16_t sk[2][kTileN * LD];
+  __shared__ __align__(16) uint16_t sv[2][kTileN * LD];
 
   const int n_wg = n_qt * g.B * g.H;
   const int wg = xcd_remap(blockIdx.x, n_wg);
@@ -81,73 +71,30 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel_16(
   float m = kNegInf, l = 0.f;
 
   const int e_beg = row_ptr[qt], e_end = row_ptr[qt + 1];
-  uint4 kreg[KP];
-  uint4 vreg[VP][4];
-
-  auto load_tile = [&](int k0) {
-#pragma unroll
-    for (int p = 0; p < KP; ++p) {
-      const int c = tid + 256 * p;
-      const int r = c / CPR, ch = c - r * CPR;
-      kreg[p] = (c < KCH && k0 + r < g.n_kv)
-                    ? *(const uint4*)(K + kb + (size_t)(k0 + r) * D + ch * 8)
-                    : make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int p = 0; p < VP; ++p) {
-      const int task = tid + 256 * p;
-      const int rg = task & 15, ch = task >> 4;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = k0 + 4 * rg + r;
-        vreg[p][r] = (task < VTASK && row < g.n_kv)
-                         ? *(const uint4*)(V + kb + (size_t)row * D + ch * 8)
-                         : make_uint4(0, 0, 0, 0);
-      }
-    }
-  };
-  auto store_tile = [&]() {
-#pragma unroll
-    for (int p = 0; p < KP; ++p) {
-      const int c = tid + 256 * p;
-      if (c < KCH) {
-        const int r = c / CPR, ch = c - r * CPR;
-        *(uint4*)(&sm.k[r * Smem::KLD + ch * 8]) = kreg[p];
-      }
-    }
-#pragma unroll
-    for (int p = 0; p < VP; ++p) {
-      const int task = tid + 256 * p;
-      if (task < VTASK) {
-        const int rg = task & 15, ch = task >> 4;
-        const uint16_t* e0 = (const uint16_t*)&vreg[p][0];
-        const uint16_t* e1 = (const uint16_t*)&vreg[p][1];
-        const uint16_t* e2 = (const uint16_t*)&vreg[p][2];
-        const uint16_t* e3 = (const uint16_t*)&vreg[p][3];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int d = ch * 8 + j;
-          const int phys = (((rg >> 1) ^ (d & 7)) << 3) + ((rg & 1) << 2);
-          uint2 w;
-          w.x = (uint32_t)e0[j] | ((uint32_t)e1[j] << 16);
-          w.y = (uint32_t)e2[j] | ((uint32_t)e3[j] << 16);
-          *(uint2*)(&sm.vt[d * kTileN + phys]) = w;
-        }
-      }
-    }
-  };
-
-  if (e_beg < e_end) load_tile((row_idx[e_beg] & kIdxMask) * kTileN);
+  Tile tk, tv;
+  if (e_beg < e_end) {
+    const int k0 = (row_idx[e_beg] & kIdxMask) * kTileN;
+    tk.load(K + kb, k0, g.n_kv, tid);
+    tv.load(V + kb, k0, g.n_kv, tid);
+    tk.store(sk[0], tid);
+    tv.store(sv[0], tid);
+  }
+  __syncthreads();
 
   const int q_hi_wave = min(q0 + 15, g.n_q - 1);
   for (int e = e_beg; e < e_end; ++e) {
+    const int buf = (e - e_beg) & 1;
     const int ent = row_idx[e];
     const int k0 = (ent & kIdxMask) * kTileN;
     const bool partial = (ent >> kPartialBit) & 1;
-    __syncthreads();
-    store_tile();
-    __syncthreads();
-    if (e + 1 < e_end) load_tile((row_idx[e + 1] & kIdxMask) * kTileN);
+    const bool has_next = e + 1 < e_end;
+    if (has_next) {
+      const int k1 = (row_idx[e + 1] & kIdxMask) * kTileN;
+      tk.load(K + kb, k1, g.n_kv, tid);
+      tv.load(V + kb, k1, g.n_kv, tid);
+    }
+    const uint16_t* ck = sk[buf];
+    const uint16_t* cv = sv[buf];
 
     floatx4 s[4];
 #pragma unroll
@@ -157,25 +104,26 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel_16(
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         const int d0 = 32 * ks + 8 * grp;
-        const uint4 a = (d0 < D) ? *(const uint4*)(&sm.k[r * Smem::KLD + d0]) : make_uint4(0, 0, 0, 0);
+        const uint4 a = (d0 < D) ? *(const uint4*)(&ck[r * LD + d0]) : make_uint4(0, 0, 0, 0);
         s[t] = T::mfma(a, qf[ks], s[t]);
       }
     }
 
     const bool need_mask = partial || (q0 + 15 >= g.n_q) || (k0 + kTileN > g.n_kv) ||
                            !tile_all_visible(g, q0, q_hi_wave, k0, k0 + kTileN - 1);
+    if (need_mask) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (!elem_valid(g, my_q, k0 + rho(t, 4 * grp + i), partial)) s[t][i] = kNegInf;
+    }
     float mx = kNegInf;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
+    for (int t = 0; t < 4; ++t)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float x = s[t][i] * g.scale_log2;
-        if (need_mask && !elem_valid(g, my_q, k0 + rho(t, 4 * grp + i), partial)) x = kNegInf;
-        s[t][i] = x;
-        mx = fmaxf(mx, x);
-      }
-    }
-    mx = wave_max16x4(mx);
+      for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[t][i]);
+    mx = wave_max16x4(mx) * g.scale_log2;      // softmax_scale > 0 (checked on the host)
     const float m_new = fmaxf(m, mx);
     const float m_use = (m_new == kNegInf) ? 0.f : m_new;
     const float alpha = __builtin_amdgcn_exp2f(m - m_use);
@@ -184,29 +132,30 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel_16(
     for (int t = 0; t < 4; ++t) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float p = __builtin_amdgcn_exp2f(s[t][i] - m_use);
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][i], g.scale_log2, -m_use));
         s[t][i] = p;
         rs += p;
       }
     }
     l = l * alpha + rs;
     m = m_new;
+    // alpha == 1 exactly when no row max of the wave moved: skipping is exact
+    if (__any(alpha != 1.f)) {
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+      for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+    }
 
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
-      float pv[8] = {s[2 * st][0], s[2 * st][1], s[2 * st][2], s[2 * st][3],
-                     s[2 * st + 1][0], s[2 * st + 1][1], s[2 * st + 1][2], s[2 * st + 1][3]};
-      const uint4 b = pack8<T>(pv);
+      const uint4 b = pack8<T>(s[2 * st], s[2 * st + 1]);
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const int d = 16 * dt + col;
-        const int phys = ((4 * st + grp) ^ (d & 7)) << 3;
-        const uint4 a = *(const uint4*)(&sm.vt[d * kTileN + phys]);
-        o[dt] = T::mfma(a, b, o[dt]);
-      }
+      for (int dt = 0; dt < DT; ++dt) o[dt] = T::mfma(lds_tr8(cv, LD, 32 * st, 16 * dt, lane), b, o[dt]);
     }
+    if (has_next) {
+      tk.store(sk[buf ^ 1], tid);
+      tv.store(sv[buf ^ 1], tid);
+    }
+    __syncthreads();
   }
 
   const float l_tot = wave_sum16x4(l);
@@ -216,8 +165,8 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel_16(
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
       uint2 w;
-      w.x = (uint32_t)T::from_float(o[dt][0] * inv) | ((uint32_t)T::from_float(o[dt][1] * inv) << 16);
-      w.y = (uint32_t)T::from_float(o[dt][2] * inv) | ((uint32_t)T::from_float(o[dt][3] * inv) << 16);
+      w.x = pack2<T>(o[dt][0] * inv, o[dt][1] * inv);
+      w.y = pack2<T>(o[dt][2] * inv, o[dt][3] * inv);
       *(uint2*)(O + qb + (size_t)my_q * D + 16 * dt + 4 * grp) = w;
     }
     if (grp == 0) LSE[(size_t)bh * g.n_q + my_q] = valid ? m * kLn2 + __logf(l_tot) : 0.f;
@@ -238,7 +187,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel_32(
   constexpr int CH = kTileN * CPR;
   constexpr int P = (CH + 255) / 256;
   using Smem = FwdSmem32<D>;
-  __shared__ Smem sm;
+  __shared__ __align__(16) Smem sm;
 
   const int n_wg = n_qt * g.B * g.H;
   const int wg = xcd_remap(blockIdx.x, n_wg);
