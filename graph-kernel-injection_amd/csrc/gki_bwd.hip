@@ -115,9 +115,8 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
   constexpr int KS = (D + 31) / 32;
   constexpr int DT = D / 16;
   using Tile = RowTile<D>;
-  constexpr int LD = Tile::LD;
-  __shared__ __align__(16) uint16_t sq[2][64 * LD];
-  __shared__ __align__(16) uint16_t sdo[2][64 * LD];
+  __shared__ __align__(16) uint16_t sq[2][64 * D];
+  __shared__ __align__(16) uint16_t sdo[2][64 * D];
   __shared__ __align__(16) float slse[2][64];
   __shared__ __align__(16) float sdlt[2][64];
 
@@ -193,8 +192,8 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         const int d0 = 32 * ks + 8 * grp;
-        const uint4 aq = (d0 < D) ? *(const uint4*)(&cq[r * LD + d0]) : make_uint4(0, 0, 0, 0);
-        const uint4 ad = (d0 < D) ? *(const uint4*)(&cdo[r * LD + d0]) : make_uint4(0, 0, 0, 0);
+        const uint4 aq = (d0 < D) ? lds_row8<D>(cq, r, d0) : make_uint4(0, 0, 0, 0);
+        const uint4 ad = (d0 < D) ? lds_row8<D>(cdo, r, d0) : make_uint4(0, 0, 0, 0);
         s = T::mfma(aq, kf[ks], s);
         dp = T::mfma(ad, vf[ks], dp);
       }
@@ -217,8 +216,8 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
       const uint4 ad = pack8<T>(ds[2 * st], ds[2 * st + 1]);
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        dv[dt] = T::mfma(ap, lds_tr8(cdo, LD, 32 * st, 16 * dt, lane), dv[dt]);
-        dk[dt] = T::mfma(ad, lds_tr8(cq, LD, 32 * st, 16 * dt, lane), dk[dt]);
+        dv[dt] = T::mfma(ap, lds_tr8<D>(cdo, 32 * st, 16 * dt, lane), dv[dt]);
+        dk[dt] = T::mfma(ad, lds_tr8<D>(cq, 32 * st, 16 * dt, lane), dk[dt]);
       }
     }
     if (has_next) store_tile(buf ^ 1);
@@ -364,9 +363,8 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_16(
   constexpr int KS = (D + 31) / 32;
   constexpr int DT = D / 16;
   using Tile = RowTile<D>;
-  constexpr int LD = Tile::LD;
-  __shared__ __align__(16) uint16_t sk[2][64 * LD];
-  __shared__ __align__(16) uint16_t sv[2][64 * LD];
+  __shared__ __align__(16) uint16_t sk[2][64 * D];
+  __shared__ __align__(16) uint16_t sv[2][64 * D];
 
   const int n_wg = n_qt * g.B * g.H;
   const int wg = xcd_remap(blockIdx.x, n_wg);
@@ -428,8 +426,8 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_16(
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         const int d0 = 32 * ks + 8 * grp;
-        const uint4 ak = (d0 < D) ? *(const uint4*)(&ck[r * LD + d0]) : make_uint4(0, 0, 0, 0);
-        const uint4 av = (d0 < D) ? *(const uint4*)(&cv[r * LD + d0]) : make_uint4(0, 0, 0, 0);
+        const uint4 ak = (d0 < D) ? lds_row8<D>(ck, r, d0) : make_uint4(0, 0, 0, 0);
+        const uint4 av = (d0 < D) ? lds_row8<D>(cv, r, d0) : make_uint4(0, 0, 0, 0);
         s = T::mfma(ak, qf[ks], s);
         dp = T::mfma(av, df[ks], dp);
       }
@@ -444,7 +442,7 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_16(
     for (int st = 0; st < 2; ++st) {
       const uint4 b = pack8<T>(ds[2 * st], ds[2 * st + 1]);
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) dq[dt] = T::mfma(lds_tr8(ck, LD, 32 * st, 16 * dt, lane), b, dq[dt]);
+      for (int dt = 0; dt < DT; ++dt) dq[dt] = T::mfma(lds_tr8<D>(ck, 32 * st, 16 * dt, lane), b, dq[dt]);
     }
     if (has_next) {
       tk.store(sk[buf ^ 1], tid);

@@ -25,6 +25,7 @@ int check_launch(const char* what) {
   return 0;
 }
 
+int fwd_tile_m(int dtype);
 int fwd_dispatch(int dtype, int head_dim, const Geom& g, const void* q, const void* k, const void* v,
                  void* o, float* lse, const int32_t* row_ptr, const int32_t* row_idx, int n_qt,
                  hipStream_t stream);
@@ -86,8 +87,11 @@ int gki_abi_version(void) { return 1; }
 
 const char* gki_last_error(void) { return g_last_error.c_str(); }
 
-int gki_tile_sizes(int32_t* tile_m, int32_t* tile_n, int32_t* decode_tile_m, int32_t* decode_max_q) {
-  if (tile_m) *tile_m = kTileM;
+int gki_tile_sizes(int32_t* fwd_tile_m_16, int32_t* fwd_tile_m_32, int32_t* bwd_tile_m,
+                   int32_t* tile_n, int32_t* decode_tile_m, int32_t* decode_max_q) {
+  if (fwd_tile_m_16) *fwd_tile_m_16 = fwd_tile_m(kBF16);
+  if (fwd_tile_m_32) *fwd_tile_m_32 = fwd_tile_m(kF32);
+  if (bwd_tile_m) *bwd_tile_m = kTileM;
   if (tile_n) *tile_n = kTileN;
   if (decode_tile_m) *decode_tile_m = kDecodeTileM;
   if (decode_max_q) *decode_max_q = kDecodeMaxQ;
@@ -104,7 +108,8 @@ int gki_bsa_fwd(const void* q, const void* k, const void* v, void* o, float* lse
                          softmax_scale, is_causal, sink_size, window_size))
     return rc;
   GKI_REQUIRE(q && k && v && o && lse && row_ptr && row_idx, 1, "gki_bsa_fwd: null pointer");
-  GKI_REQUIRE(n_qt == (n_q + kTileM - 1) / kTileM, 1, "gki_bsa_fwd: schedule row count mismatch");
+  const int tm = fwd_tile_m(dtype);
+  GKI_REQUIRE(n_qt == (n_q + tm - 1) / tm, 1, "gki_bsa_fwd: schedule row count mismatch");
   return fwd_dispatch(dtype, head_dim, g, q, k, v, o, lse, row_ptr, row_idx, n_qt, (hipStream_t)stream);
 }
 

@@ -98,33 +98,59 @@ __device__ inline uint4 pack8(const floatx4& lo, const floatx4& hi) {
                     pack2<T>(hi[2], hi[3]));
 }
 
-// Transposed MFMA operand from a row-major 16-bit LDS tile with `ld` elements
-// per row, via ds_read_b64_tr_b16: within each 16-lane group, lane l points at
-// row k0 + l/4, columns n0 + 4*(l%4) .. +3, and the instruction hands lane i
-// column n0 + i of those four rows. Two reads give lane (g, c) = (lane/16,
-// lane%16) the 8 elements tile[k0 + 8g + e][n0 + c], e = 0..7: the K-operand
-// layout of v_mfma_f32_16x16x32_{bf16,f16} for a matrix stored K-major.
+// LDS tile layout for 16-bit [64][D] tiles: row-major, no padding, 16-byte
+// chunks XOR-swizzled per row by swz(row) = 2*(row&3) + ((row>>3)&1) (kept
+// below the chunk count). Conflict-free for both access patterns the kernels
+// use: 16-byte reads of rows {b..b+3, b+8..b+11} at one chunk (the rho() row
+// order), and ds_read_b64_tr_b16 over 4 consecutive rows x 2 adjacent chunks.
+template <int D>
+__device__ inline int lds_off(int row, int col) {
+  constexpr int CPR = D / 8;
+  const int sw = (2 * (row & 3) + ((row >> 3) & 1)) & (CPR - 1);
+  return row * D + ((((col >> 3) ^ sw)) << 3) + (col & 7);
+}
+
+// Transposed MFMA operand from a swizzled 16-bit LDS tile via
+// ds_read_b64_tr_b16: within each 16-lane group, lane l points at row
+// k0 + l/4, columns n0 + 4*(l%4) .. +3, and the instruction hands lane i column
+// n0 + i of those four rows. Two reads give lane (g, c) = (lane/16, lane%16)
+// the 8 elements tile[k0 + 8g + e][n0 + c], e = 0..7: the K-operand layout of
+// v_mfma_f32_16x16x32_{bf16,f16} for a matrix stored K-major. (k0 is a
+// multiple of 32, so rows r and r+4 share a swizzle.)
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
-__device__ inline uint4 lds_tr8(const uint16_t* tile, int ld, int k0, int n0, int lane) {
+template <int D>
+__device__ inline uint4 lds_tr8(const uint16_t* tile, int k0, int n0, int lane) {
   const int g = lane >> 4, l = lane & 15;
-  const uint16_t* p = tile + (k0 + 8 * g + (l >> 2)) * ld + n0 + 4 * (l & 3);
+  const uint16_t* p = tile + lds_off<D>(k0 + 8 * g + (l >> 2), n0 + 4 * (l & 3));
   const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)p);
-  const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(p + 4 * ld));
+  const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(p + 4 * D));
   const uint2 a = __builtin_bit_cast(uint2, lo), b = __builtin_bit_cast(uint2, hi);
   return make_uint4(a.x, a.y, b.x, b.y);
+}
+// 16-byte row read (8 elements starting at a multiple-of-8 column).
+template <int D>
+__device__ inline uint4 lds_row8(const uint16_t* tile, int row, int col) {
+  return *(const uint4*)(tile + lds_off<D>(row, col));
 }
 
 // Stage a 64-row tile of a row-major [n, D] 16-bit matrix: each thread moves
 // P 16-byte chunks, consecutive threads covering consecutive bytes of a row.
 template <int D>
 struct RowTile {
-  static constexpr int LD = D + 8;           // padded LDS row (elements)
   static constexpr int CPR = D / 8;          // 16-byte chunks per row
   static constexpr int CH = 64 * CPR;
   static constexpr int P = (CH + 255) / 256;
   uint4 reg[P];
   __device__ inline void load(const uint16_t* base, int r0, int n_rows, int tid) {
+    if (CH % 256 == 0 && r0 + 64 <= n_rows) {   // interior tile: no predicates
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        const int c = tid + 256 * p;
+        reg[p] = *(const uint4*)(base + (size_t)(r0 + c / CPR) * D + (c % CPR) * 8);
+      }
+      return;
+    }
 #pragma unroll
     for (int p = 0; p < P; ++p) {
       const int c = tid + 256 * p;
@@ -137,21 +163,20 @@ struct RowTile {
 #pragma unroll
     for (int p = 0; p < P; ++p) {
       const int c = tid + 256 * p;
-      if (c < CH) {
-        const int r = c / CPR, ch = c - r * CPR;
-        *(uint4*)(&lds[r * LD + ch * 8]) = reg[p];
-      }
+      if (c < CH) *(uint4*)(lds + lds_off<D>(c / CPR, (c % CPR) * 8)) = reg[p];
     }
   }
 };
 
 // ---------------------------------------------------------------------------
-// Kernel tiling. All prefill / backward kernels use 64x64 (q x kv) tiles, four
-// waves per workgroup, each wave owning 16 rows of the tile's outer axis. The
-// decode kernel (n_q <= kDecodeMaxQ) uses a single 16-row q tile.
+// Kernel tiling. The forward uses 128x64 (q x kv) tiles, four waves per
+// workgroup, each wave owning 32 query rows; the backward kernels use 64x64
+// tiles, each wave owning 16 rows of the tile's outer axis. The decode kernel
+// (n_q <= kDecodeMaxQ) uses a single 16-row q tile.
 // ---------------------------------------------------------------------------
-constexpr int kTileM = 64;
-constexpr int kTileN = 64;
+constexpr int kTileM = 64;       // q rows of the dQ / dK-dV tiles
+constexpr int kTileN = 64;       // kv rows of every tile
+constexpr int kTileMF = 128;     // q rows of the forward tile (4 waves x 32 rows)
 constexpr int kDecodeTileM = 16;
 constexpr int kDecodeMaxQ = 4;
 constexpr int kPartialBit = 30;       // schedule entry flag: needs per-element mask lookup
@@ -183,12 +208,31 @@ __device__ inline bool token_visible(int q_abs, int k, int sink, int window) {
   return (k <= q_abs) && (k < sink || k >= q_abs - window + 1);
 }
 
-// Full element predicate for (q row, kv column) of a tile flagged "needs mask".
+// Bounds + token predicate for (q row, kv column), branch-free.
+__device__ inline bool elem_tok(const Geom& g, int q_row, int kv) {
+  const int qa = q_row + g.q_off;
+  const bool in = (q_row < g.n_q) & (kv < g.n_kv);
+  const bool vis = (kv <= qa) & ((kv < g.sink) | (kv >= qa - g.window + 1));
+  return in & ((g.causal == 0) | vis);
+}
+
+// Full element predicate for (q row, kv column) of a tile flagged "needs mask":
+// tiles flagged partial also consult the lifted block mask.
 __device__ inline bool elem_valid(const Geom& g, int q_row, int kv, bool partial) {
-  if (q_row >= g.n_q || kv >= g.n_kv) return false;
-  if (g.causal && !token_visible(q_row + g.q_off, kv, g.sink, g.window)) return false;
-  if (partial && g.mask[(size_t)(q_row / g.bm) * g.n_kb + kv / g.bn] == 0) return false;
-  return true;
+  bool ok = elem_tok(g, q_row, kv);
+  if (partial && ok) ok = g.mask[(size_t)(q_row / g.bm) * g.n_kb + kv / g.bn] != 0;
+  return ok;
+}
+
+// Is some (q, k) with q in [q_lo, q_hi], k in [k_lo, k_hi] (inclusive, absolute
+// positions, non-empty) visible under the token rule (k <= q) & (k < S | k >= q-W+1)?
+__device__ inline bool any_visible(long q_lo, long q_hi, long k_lo, long k_hi, long sink, long window) {
+  const bool sink_part = k_lo < sink && k_lo <= q_hi;
+  // window: some q with max(k_lo, q-W+1) <= min(k_hi, q)
+  const long qa = q_lo > k_lo ? q_lo : k_lo;
+  const long qb = q_hi < k_hi + window - 1 ? q_hi : k_hi + window - 1;
+  const bool window_part = window >= 1 && qa <= qb;
+  return sink_part || window_part;
 }
 
 // True when every (q, kv) with q in [q_lo, q_hi], kv in [k_lo, k_hi] (inclusive,

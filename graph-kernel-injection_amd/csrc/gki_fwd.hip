@@ -7,34 +7,27 @@
 // O = acc / l, LSE = m + ln(l) with the (O = 0, LSE = 0) sentinel for rows that
 // saw no key (sparse_triton_kernel.py:341-352).
 //
-// Design (one workgroup = 4 waves = one 64-row q tile, wave w owns rows 16w..16w+15):
-//  * S^T = K Q^T on v_mfma_f32_16x16x32_{bf16,f16} (v_mfma_f32_16x16x4f32 for
-//    fp32). In the accumulator layout lane (g, c) holds q row c, so the running
-//    max / sum are per-lane scalars; row reductions need two cross-group shuffles.
+// 16-bit design (one workgroup = 4 waves = one 128-row q tile; wave w owns rows
+// 32w .. 32w+31 as two 16-row blocks h = 0, 1):
+//  * S^T = K Q^T on v_mfma_f32_16x16x32_{bf16,f16}. In the accumulator layout
+//    lane (g, c) holds q row c of its block, so the running max / sum are
+//    per-lane scalars; row reductions need two cross-group shuffles.
+//  * Every K / V^T operand read from LDS feeds the MFMAs of both row blocks:
+//    LDS traffic per flop is half that of 16 rows per wave.
 //  * K tile rows are fetched through the rho() permutation, which makes the S^T
-//    accumulators of subtiles (2s, 2s+1) the B operand of O^T += V^T P^T as-is.
-//  * K and V tiles are staged row-major in LDS with coalesced 16-byte loads,
-//    double-buffered (one barrier per tile; the next tile's global loads are in
-//    flight during the current tile's MFMAs). V^T operands are read with the
-//    gfx950 LDS transpose read (ds_read_b64_tr_b16).
-//  * The O^T rescale is skipped, exactly, when no row max of the wave moved.
-//  * Only kept tiles are visited: the workgroup walks a GPU-resident CSR list.
+//    accumulators of subtiles (2s, 2s+1) the B operand of O^T += V^T P^T as-is;
+//    V^T operands come from the gfx950 LDS transpose read (ds_read_b64_tr_b16).
+//  * K and V tiles are staged row-major (XOR-swizzled chunks, conflict-free for
+//    both read patterns) with coalesced 16-byte loads, double-buffered: one
+//    barrier per tile, the next tile's global loads in flight during the MFMAs.
+//  * Only kept tiles are visited (GPU-resident CSR list); the O^T rescale is
+//    skipped, exactly, when no row max of a block moved.
+// The fp32 path uses v_mfma_f32_16x16x4f32 on 64-row tiles (16 rows per wave).
 #include "gki_common.cuh"
 
 namespace gki {
 namespace {
 
-template <int D>
-struct FwdSmem32 {
-  static constexpr int LD = D + 4;
-  float k[kTileN * LD];
-  float v[kTileN * LD];
-};
-
-// ---------------------------------------------------------------------------
-// 16-bit path: K and V tiles row-major in LDS (double-buffered, one barrier per
-// tile); V^T operands come from ds_read_b64_tr_b16 (lds_tr8).
-// ---------------------------------------------------------------------------
 template <typename T, int D>
 __global__ __launch_bounds__(256, 2) void fwd_kernel_16(
     Geom g, const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
@@ -43,9 +36,8 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel_16(
   constexpr int KS = (D + 31) / 32;   // k-steps of the QK^T contraction
   constexpr int DT = D / 16;          // 16-row tiles of O^T
   using Tile = RowTile<D>;
-  constexpr int LD = Tile::LD;
-  __shared__ __align__(16) uint16_t sk[2][kTileN * LD];
-  __shared__ __align__(16) uint16_t sv[2][kTileN * LD];
+  __shared__ __align__(16) uint16_t sk[2][kTileN * D];
+  __shared__ __align__(16) uint16_t sv[2][kTileN * D];
 
   const int n_wg = n_qt * g.B * g.H;
   const int wg = xcd_remap(blockIdx.x, n_wg);
@@ -54,21 +46,26 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel_16(
   const size_t kb = (size_t)bh * g.n_kv * D;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int grp = lane >> 4, col = lane & 15;
-  const int q0 = qt * kTileM + wave * 16;
-  const int my_q = q0 + col;
+  const int qw = qt * kTileMF + wave * 32;   // first row of this wave
 
-  uint4 qf[KS];
+  uint4 qf[2][KS];
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    const int d0 = 32 * ks + 8 * grp;
-    qf[ks] = (my_q < g.n_q && d0 < D) ? *(const uint4*)(Q + qb + (size_t)my_q * D + d0)
-                                      : make_uint4(0, 0, 0, 0);
+  for (int h = 0; h < 2; ++h) {
+    const int q = qw + 16 * h + col;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int d0 = 32 * ks + 8 * grp;
+      qf[h][ks] = (q < g.n_q && d0 < D) ? *(const uint4*)(Q + qb + (size_t)q * D + d0)
+                                        : make_uint4(0, 0, 0, 0);
+    }
   }
 
-  floatx4 o[DT];
+  floatx4 o[2][DT];
 #pragma unroll
-  for (int i = 0; i < DT; ++i) o[i] = floatx4{0.f, 0.f, 0.f, 0.f};
-  float m = kNegInf, l = 0.f;
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int i = 0; i < DT; ++i) o[h][i] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float m[2] = {kNegInf, kNegInf}, l[2] = {0.f, 0.f};
 
   const int e_beg = row_ptr[qt], e_end = row_ptr[qt + 1];
   Tile tk, tv;
@@ -81,7 +78,6 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel_16(
   }
   __syncthreads();
 
-  const int q_hi_wave = min(q0 + 15, g.n_q - 1);
   for (int e = e_beg; e < e_end; ++e) {
     const int buf = (e - e_beg) & 1;
     const int ent = row_idx[e];
@@ -96,60 +92,71 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel_16(
     const uint16_t* ck = sk[buf];
     const uint16_t* cv = sv[buf];
 
-    floatx4 s[4];
+    floatx4 s[2][4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      s[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+      s[0][t] = s[1][t] = floatx4{0.f, 0.f, 0.f, 0.f};
       const int r = rho(t, col);
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         const int d0 = 32 * ks + 8 * grp;
-        const uint4 a = (d0 < D) ? *(const uint4*)(&ck[r * LD + d0]) : make_uint4(0, 0, 0, 0);
-        s[t] = T::mfma(a, qf[ks], s[t]);
+        const uint4 a = (d0 < D) ? lds_row8<D>(ck, r, d0) : make_uint4(0, 0, 0, 0);
+        s[0][t] = T::mfma(a, qf[0][ks], s[0][t]);
+        s[1][t] = T::mfma(a, qf[1][ks], s[1][t]);
       }
     }
 
-    const bool need_mask = partial || (q0 + 15 >= g.n_q) || (k0 + kTileN > g.n_kv) ||
-                           !tile_all_visible(g, q0, q_hi_wave, k0, k0 + kTileN - 1);
-    if (need_mask) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int q0 = qw + 16 * h;
+      const bool need_mask = partial || (q0 + 15 >= g.n_q) || (k0 + kTileN > g.n_kv) ||
+                             !tile_all_visible(g, q0, min(q0 + 15, g.n_q - 1), k0, k0 + kTileN - 1);
+      if (need_mask) {
+        const int my_q = q0 + col;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (!elem_valid(g, my_q, k0 + rho(t, 4 * grp + i), partial)) s[h][t][i] = kNegInf;
+      }
+      float mx = kNegInf;
 #pragma unroll
       for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (!elem_valid(g, my_q, k0 + rho(t, 4 * grp + i), partial)) s[t][i] = kNegInf;
-    }
-    float mx = kNegInf;
+        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[h][t][i]);
+      mx = wave_max16x4(mx) * g.scale_log2;     // softmax_scale > 0 (checked on the host)
+      const float m_new = fmaxf(m[h], mx);
+      const float m_use = (m_new == kNegInf) ? 0.f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m[h] - m_use);
+      float rs = 0.f;
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+      for (int t = 0; t < 4; ++t) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[t][i]);
-    mx = wave_max16x4(mx) * g.scale_log2;      // softmax_scale > 0 (checked on the host)
-    const float m_new = fmaxf(m, mx);
-    const float m_use = (m_new == kNegInf) ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m - m_use);
-    float rs = 0.f;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][i], g.scale_log2, -m_use));
-        s[t][i] = p;
-        rs += p;
+        for (int i = 0; i < 4; ++i) {
+          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[h][t][i], g.scale_log2, -m_use));
+          s[h][t][i] = p;
+          rs += p;
+        }
       }
-    }
-    l = l * alpha + rs;
-    m = m_new;
-    // alpha == 1 exactly when no row max of the wave moved: skipping is exact
-    if (__any(alpha != 1.f)) {
+      l[h] = l[h] * alpha + rs;
+      m[h] = m_new;
+      // alpha == 1 exactly when no row max of the block moved: skipping is exact
+      if (__any(alpha != 1.f)) {
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+        for (int dt = 0; dt < DT; ++dt) o[h][dt] *= alpha;
+      }
     }
 
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
-      const uint4 b = pack8<T>(s[2 * st], s[2 * st + 1]);
+      const uint4 b0 = pack8<T>(s[0][2 * st], s[0][2 * st + 1]);
+      const uint4 b1 = pack8<T>(s[1][2 * st], s[1][2 * st + 1]);
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) o[dt] = T::mfma(lds_tr8(cv, LD, 32 * st, 16 * dt, lane), b, o[dt]);
+      for (int dt = 0; dt < DT; ++dt) {
+        const uint4 a = lds_tr8<D>(cv, 32 * st, 16 * dt, lane);
+        o[0][dt] = T::mfma(a, b0, o[0][dt]);
+        o[1][dt] = T::mfma(a, b1, o[1][dt]);
+      }
     }
     if (has_next) {
       tk.store(sk[buf ^ 1], tid);
@@ -158,24 +165,35 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel_16(
     __syncthreads();
   }
 
-  const float l_tot = wave_sum16x4(l);
-  const bool valid = l_tot > 0.f;
-  const float inv = valid ? 1.f / l_tot : 1.f;
-  if (my_q < g.n_q) {
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      uint2 w;
-      w.x = pack2<T>(o[dt][0] * inv, o[dt][1] * inv);
-      w.y = pack2<T>(o[dt][2] * inv, o[dt][3] * inv);
-      *(uint2*)(O + qb + (size_t)my_q * D + 16 * dt + 4 * grp) = w;
+  for (int h = 0; h < 2; ++h) {
+    const int my_q = qw + 16 * h + col;
+    const float l_tot = wave_sum16x4(l[h]);
+    const bool valid = l_tot > 0.f;
+    const float inv = valid ? 1.f / l_tot : 1.f;
+    if (my_q < g.n_q) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        uint2 w;
+        w.x = pack2<T>(o[h][dt][0] * inv, o[h][dt][1] * inv);
+        w.y = pack2<T>(o[h][dt][2] * inv, o[h][dt][3] * inv);
+        *(uint2*)(O + qb + (size_t)my_q * D + 16 * dt + 4 * grp) = w;
+      }
+      if (grp == 0) LSE[(size_t)bh * g.n_q + my_q] = valid ? m[h] * kLn2 + __logf(l_tot) : 0.f;
     }
-    if (grp == 0) LSE[(size_t)bh * g.n_q + my_q] = valid ? m * kLn2 + __logf(l_tot) : 0.f;
   }
 }
 
 // ---------------------------------------------------------------------------
-// fp32 path (v_mfma_f32_16x16x4f32): K and V stay row-major in LDS.
+// fp32 path (v_mfma_f32_16x16x4f32, 64-row tiles): K and V stay row-major in LDS.
 // ---------------------------------------------------------------------------
+template <int D>
+struct FwdSmem32 {
+  static constexpr int LD = D + 4;
+  float k[kTileN * LD];
+  float v[kTileN * LD];
+};
+
 template <int D>
 __global__ __launch_bounds__(256, 2) void fwd_kernel_32(
     Geom g, const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
@@ -331,6 +349,8 @@ int launch_fwd(int dtype, const Geom& g, const void* q, const void* k, const voi
 }
 
 }  // namespace
+
+int fwd_tile_m(int dtype) { return dtype == kF32 ? kTileM : kTileMF; }
 
 int fwd_dispatch(int dtype, int head_dim, const Geom& g, const void* q, const void* k, const void* v,
                  void* o, float* lse, const int32_t* row_ptr, const int32_t* row_idx, int n_qt,

@@ -7,8 +7,10 @@
 //   (unclipped, ceil-div grid). Bit-exact with the reference formula.
 // * dense_mask_kernel restates `make_dense_mask` (sparse_triton_kernel.py:184-210).
 // * tile_mask_kernel maps a mask of any (bm, bn) granularity onto the kernels'
-//   fixed tm x tn tiles: 0 = skip, 1 = every overlapping mask block kept,
-//   2 = partially kept (the kernel then looks the mask up per element).
+//   fixed tm x tn tiles, taking the token rule into account when causal:
+//   0 = nothing to compute, 1 = the lifted mask keeps every element the token
+//   rule allows, 2 = partially kept (the kernel then looks the mask up per
+//   element).
 // * The list kernels turn a {0,1,2} matrix into CSR (rows -> ascending columns)
 //   and CSC (columns -> ascending rows) int32 lists, entry = index | (v==2)<<30.
 //   Applied to a 0/1 block mask they give exactly `mask.nonzero()` order.
@@ -43,25 +45,34 @@ __global__ void dense_mask_kernel(int32_t* __restrict__ mask, int64_t bm, int64_
   mask[idx] = (!causal || (j * bn < (i + 1) * bm)) ? 1 : 0;
 }
 
+// Tile (a, b) of tm x tn is visited (1) if some in-bounds element is kept by the
+// lifted block mask and allowed by the token rule (when causal), and partial
+// (2) if additionally some in-bounds element allowed by the token rule is NOT
+// kept by the lifted mask, so the kernel must consult the mask per element.
 __global__ void tile_mask_kernel(const int32_t* __restrict__ mask, int n_qb, int n_kb, int bm, int bn,
-                                 int n_q, int n_kv, int tm, int tn, int n_qt, int n_kt,
-                                 int32_t* __restrict__ tmask) {
+                                 int n_q, int n_kv, int tm, int tn, int n_qt, int n_kt, int causal,
+                                 int sink, int window, int32_t* __restrict__ tmask) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= (int64_t)n_qt * n_kt) return;
   const int a = (int)(idx / n_kt), b = (int)(idx - (int64_t)a * n_kt);
   const int qr0 = a * tm, qr1 = min((a + 1) * tm, n_q) - 1;
   const int kc0 = b * tn, kc1 = min((b + 1) * tn, n_kv) - 1;
-  int out = 0;
+  const long off = (long)n_kv - n_q;
+  bool visited = false, partial = false;
   if (qr0 <= qr1 && kc0 <= kc1) {
-    const int r0 = qr0 / bm, r1 = qr1 / bm;
-    const int c0 = kc0 / bn, c1 = kc1 / bn;
-    int kept = 0;
-    for (int r = r0; r <= r1; ++r)
-      for (int c = c0; c <= c1; ++c) kept += mask[(size_t)r * n_kb + c] != 0;
-    const int total = (r1 - r0 + 1) * (c1 - c0 + 1);
-    out = kept == 0 ? 0 : (kept == total ? 1 : 2);
+    for (int r = qr0 / bm; r <= qr1 / bm; ++r) {
+      const int rq0 = max(qr0, r * bm), rq1 = min(qr1, (r + 1) * bm - 1);
+      for (int c = kc0 / bn; c <= kc1 / bn; ++c) {
+        const int ck0 = max(kc0, c * bn), ck1 = min(kc1, (c + 1) * bn - 1);
+        if (causal && !any_visible(rq0 + off, rq1 + off, ck0, ck1, sink, window)) continue;
+        if (mask[(size_t)r * n_kb + c] != 0)
+          visited = true;
+        else
+          partial = true;
+      }
+    }
   }
-  tmask[idx] = out;
+  tmask[idx] = visited ? (partial ? 2 : 1) : 0;
 }
 
 __global__ __launch_bounds__(256) void row_count_kernel(const int32_t* __restrict__ m, int n_cols,
@@ -224,17 +235,18 @@ int gki_dense_mask(int32_t* mask, int64_t n_q, int64_t n_kv, int64_t block_m, in
 }
 
 int gki_tile_mask(const int32_t* mask, int32_t n_qb, int32_t n_kb, int32_t block_m, int32_t block_n,
-                  int32_t n_q, int32_t n_kv, int32_t tile_m, int32_t tile_n, int32_t* tile_mask,
-                  void* stream) {
+                  int32_t n_q, int32_t n_kv, int32_t tile_m, int32_t tile_n, int32_t is_causal,
+                  int32_t sink_size, int32_t window_size, int32_t* tile_mask, void* stream) {
   GKI_REQUIRE(mask && tile_mask, 1, "gki_tile_mask: null pointer");
   GKI_REQUIRE(n_q > 0 && n_kv > 0 && block_m > 0 && block_n > 0 && tile_m > 0 && tile_n > 0, 1,
               "gki_tile_mask: sizes must be positive");
   GKI_REQUIRE(n_qb == (n_q + block_m - 1) / block_m && n_kb == (n_kv + block_n - 1) / block_n, 1,
               "gki_tile_mask: mask shape does not match ceil(n/block)");
+  GKI_REQUIRE(sink_size >= 0 && window_size >= 0, 1, "gki_tile_mask: negative sink/window");
   const int n_qt = (n_q + tile_m - 1) / tile_m, n_kt = (n_kv + tile_n - 1) / tile_n;
   hipLaunchKernelGGL(tile_mask_kernel, dim3(blocks_for((int64_t)n_qt * n_kt, 256)), dim3(256), 0,
                      (hipStream_t)stream, mask, n_qb, n_kb, block_m, block_n, n_q, n_kv, tile_m,
-                     tile_n, n_qt, n_kt, tile_mask);
+                     tile_n, n_qt, n_kt, is_causal ? 1 : 0, sink_size, window_size, tile_mask);
   return check_launch("gki_tile_mask");
 }
 

@@ -23,11 +23,10 @@ _c_float = ctypes.c_float
 SIGNATURES = {
     "gki_abi_version": (ctypes.c_int, []),
     "gki_last_error": (ctypes.c_char_p, []),
-    "gki_tile_sizes": (ctypes.c_int, [_c_ptr] * 4),
+    "gki_tile_sizes": (ctypes.c_int, [_c_ptr] * 6),
     "gki_streaming_mask": (ctypes.c_int, [_c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr]),
     "gki_dense_mask": (ctypes.c_int, [_c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_ptr]),
-    "gki_tile_mask": (ctypes.c_int, [_c_ptr, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
-                                     _c_int, _c_ptr, _c_ptr]),
+    "gki_tile_mask": (ctypes.c_int, [_c_ptr] + [_c_int] * 11 + [_c_ptr, _c_ptr]),
     "gki_block_list_counts": (ctypes.c_int, [_c_ptr, _c_int, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
                                              _c_ptr]),
     "gki_block_list_fill": (ctypes.c_int, [_c_ptr, _c_int, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
@@ -101,8 +100,9 @@ def tile_sizes() -> dict:
     global _TILE_SIZES
     if _TILE_SIZES is None:
         lib = load()
-        vals = [ctypes.c_int32() for _ in range(4)]
+        vals = [ctypes.c_int32() for _ in range(6)]
         lib.gki_tile_sizes(*[ctypes.byref(v) for v in vals])
-        keys = ("tile_m", "tile_n", "decode_tile_m", "decode_max_q")
+        keys = ("fwd_tile_m_16", "fwd_tile_m_32", "bwd_tile_m", "tile_n", "decode_tile_m",
+                "decode_max_q")
         _TILE_SIZES = {k: int(v.value) for k, v in zip(keys, vals)}
-    return dict(_TILE_SIZES)
+    return _TILE_SIZES

@@ -7,10 +7,13 @@ mask is turned once, on the GPU, into int32 lists:
 * ``build_block_lists(mask)`` -- CSR (row -> ascending kept columns) and CSC
   (column -> ascending kept rows) of a 0/1 block mask. The CSR order is exactly
   ``mask.nonzero()``.
-* ``prefill_schedule(...)`` -- the same lists over the kernels' fixed 64x64
-  tiles (a mask of any block size is first classified per tile by
-  ``gki_tile_mask``), plus the "heavy columns first" order for the dK/dV grid.
-* ``decode_schedule(...)`` -- the kept kv tiles of the single decode q tile.
+* ``fwd_schedule`` / ``bwd_schedule`` / ``decode_schedule`` -- the same lists
+  over the kernels' fixed tiles (forward 128x64 for 16-bit inputs, 64x64 for
+  fp32; backward 64x64; decode 16x64). A mask of any block size is first
+  classified per tile by ``gki_tile_mask`` (token-rule aware when causal, so
+  tiles with nothing visible are not visited). The backward schedule adds the
+  "heavy columns first" order for the dK/dV grid; the decode schedule adds the
+  token-exact stream of visible positions.
 
 Schedules are cached per mask tensor (identity, version, geometry); the cache
 holds a reference to the mask so its storage cannot be recycled under the key.
@@ -43,8 +46,14 @@ class BlockLists:
 
 
 @dataclass(frozen=True)
-class PrefillSchedule:
-    lists: BlockLists         # over kernel tiles (n_qt x n_kt)
+class FwdSchedule:
+    lists: BlockLists         # CSR used; over fwd tiles (n_qt x n_kt)
+    n_qt: int
+
+
+@dataclass(frozen=True)
+class BwdSchedule:
+    lists: BlockLists         # over 64x64 tiles (n_qt x n_kt)
     kv_order: torch.Tensor    # [n_kt] int32, heavy columns first
     n_heavy: int
     n_qt: int
@@ -63,7 +72,7 @@ def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
-def _lists_of(matrix: torch.Tensor) -> BlockLists:
+def _lists_of(matrix: torch.Tensor, need_cols: bool = True) -> BlockLists:
     """CSR/CSC of a {0,1,2}-valued int32 device matrix (2 marks partial)."""
     lib = _lib.load()
     n_rows, n_cols = (int(s) for s in matrix.shape)
@@ -80,8 +89,9 @@ def _lists_of(matrix: torch.Tensor) -> BlockLists:
     row_idx = torch.empty(max(nnz, 1), dtype=torch.int32, device=dev)
     col_idx = torch.empty(max(nnz, 1), dtype=torch.int32, device=dev)
     _lib.check(lib.gki_block_list_fill(matrix.data_ptr(), n_rows, n_cols, row_ptr.data_ptr(),
-                                       col_ptr.data_ptr(), row_idx.data_ptr(), col_idx.data_ptr(),
-                                       stream), "gki_block_list_fill")
+                                       col_ptr.data_ptr(), row_idx.data_ptr(),
+                                       col_idx.data_ptr() if need_cols else None, stream),
+               "gki_block_list_fill")
     return BlockLists(row_ptr, row_idx[:nnz], col_ptr, col_idx[:nnz], n_rows, n_cols, nnz)
 
 
@@ -101,14 +111,16 @@ def build_block_lists(block_mask: torch.Tensor) -> BlockLists:
         return _lists_of(m)
 
 
-def _tile_matrix(mask: torch.Tensor, n_q: int, n_kv: int, block_m: int, block_n: int,
-                 tile_m: int, tile_n: int) -> torch.Tensor:
+def tile_matrix(mask: torch.Tensor, n_q: int, n_kv: int, block_m: int, block_n: int, tile_m: int,
+                tile_n: int, is_causal: bool, sink: int, window: int) -> torch.Tensor:
+    """{0, 1, 2} classification of the tile_m x tile_n tiles (see gki_tile_mask)."""
     lib = _lib.load()
     n_qb, n_kb = (int(s) for s in mask.shape)
     n_qt, n_kt = -(-n_q // tile_m), -(-n_kv // tile_n)
     out = torch.empty((n_qt, n_kt), dtype=torch.int32, device=mask.device)
     _lib.check(lib.gki_tile_mask(mask.data_ptr(), n_qb, n_kb, block_m, block_n, n_q, n_kv, tile_m,
-                                 tile_n, out.data_ptr(), _stream(mask.device)), "gki_tile_mask")
+                                 tile_n, int(bool(is_causal)), sink, window, out.data_ptr(),
+                                 _stream(mask.device)), "gki_tile_mask")
     return out
 
 
@@ -119,7 +131,7 @@ class _ScheduleCache:
         self._lock = threading.Lock()
 
     def get(self, mask: torch.Tensor, key: tuple, build):
-        full = (mask.data_ptr(), mask._version, tuple(mask.shape), str(mask.device)) + key
+        full = (mask.data_ptr(), mask._version, tuple(mask.shape), mask.device) + key
         with self._lock:
             hit = self._d.get(full)
             if hit is not None and hit[0] is mask:
@@ -145,23 +157,40 @@ def clear_schedule_cache() -> None:
     _CACHE.clear()
 
 
-def prefill_schedule(mask: torch.Tensor, n_q: int, n_kv: int, block_m: int,
-                     block_n: int) -> PrefillSchedule:
-    """Schedules for the prefill forward, dQ and dK/dV kernels (64x64 tiles)."""
+def fwd_schedule(mask: torch.Tensor, n_q: int, n_kv: int, block_m: int, block_n: int,
+                 is_causal: bool, sink: int, window: int, fp32: bool) -> FwdSchedule:
+    """CSR schedule of the prefill forward kernel."""
     ts = _lib.tile_sizes()
-    tm, tn = ts["tile_m"], ts["tile_n"]
+    tm = ts["fwd_tile_m_32"] if fp32 else ts["fwd_tile_m_16"]
+    tn = ts["tile_n"]
 
-    def build() -> PrefillSchedule:
+    def build() -> FwdSchedule:
+        tiles = tile_matrix(mask, n_q, n_kv, block_m, block_n, tm, tn, is_causal, sink, window)
+        lists = _lists_of(tiles, need_cols=False)
+        return FwdSchedule(lists, lists.n_rows)
+
+    key = ("fwd", n_q, n_kv, block_m, block_n, tm, tn, bool(is_causal), sink, window)
+    return _CACHE.get(mask, key, build)
+
+
+def bwd_schedule(mask: torch.Tensor, n_q: int, n_kv: int, block_m: int, block_n: int,
+                 is_causal: bool, sink: int, window: int) -> BwdSchedule:
+    """CSR + CSC schedules of the dQ and dK/dV kernels (64x64 tiles)."""
+    ts = _lib.tile_sizes()
+    tm, tn = ts["bwd_tile_m"], ts["tile_n"]
+
+    def build() -> BwdSchedule:
         lib = _lib.load()
-        tiles = _tile_matrix(mask, n_q, n_kv, block_m, block_n, tm, tn)
+        tiles = tile_matrix(mask, n_q, n_kv, block_m, block_n, tm, tn, is_causal, sink, window)
         lists = _lists_of(tiles)
         order = torch.empty(lists.n_cols, dtype=torch.int32, device=mask.device)
         n_heavy = torch.empty(1, dtype=torch.int32, device=mask.device)
         _lib.check(lib.gki_heavy_order(lists.col_ptr.data_ptr(), lists.n_cols, order.data_ptr(),
                                        n_heavy.data_ptr(), _stream(mask.device)), "gki_heavy_order")
-        return PrefillSchedule(lists, order, int(n_heavy.item()), lists.n_rows, lists.n_cols)
+        return BwdSchedule(lists, order, int(n_heavy.item()), lists.n_rows, lists.n_cols)
 
-    return _CACHE.get(mask, ("prefill", n_q, n_kv, block_m, block_n, tm, tn), build)
+    key = ("bwd", n_q, n_kv, block_m, block_n, tm, tn, bool(is_causal), sink, window)
+    return _CACHE.get(mask, key, build)
 
 
 def decode_schedule(mask: torch.Tensor, n_q: int, n_kv: int, block_m: int, block_n: int,
@@ -173,8 +202,8 @@ def decode_schedule(mask: torch.Tensor, n_q: int, n_kv: int, block_m: int, block
 
     def build() -> DecodeSchedule:
         lib = _lib.load()
-        tiles = _tile_matrix(mask, n_q, n_kv, block_m, block_n, tm, tn)
-        lists = _lists_of(tiles)
+        tiles = tile_matrix(mask, n_q, n_kv, block_m, block_n, tm, tn, is_causal, sink, window)
+        lists = _lists_of(tiles, need_cols=False)
         tokens = torch.empty(max(lists.nnz * tn, 1), dtype=torch.int32, device=mask.device)
         count = torch.zeros(1, dtype=torch.int32, device=mask.device)
         n_qb, n_kb = (int(s) for s in mask.shape)

@@ -21,7 +21,7 @@ from typing import Optional, Tuple
 import torch
 
 from . import _lib
-from .lists import _CACHE, decode_schedule, prefill_schedule
+from .lists import _CACHE, bwd_schedule, decode_schedule, fwd_schedule
 
 _DTYPE_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 _HEAD_DIMS = (16, 32, 64, 128)
@@ -120,7 +120,8 @@ class _BlockSparseFlashAttention(torch.autograd.Function):
                     B, H, N_Q, N_KV, D, sched.tokens.data_ptr(), sched.n_tokens, *common,
                     ws_ptr, n_splits, stream), "gki_bsa_decode")
             else:
-                sched = prefill_schedule(block_mask, N_Q, N_KV, block_m, block_n)
+                sched = fwd_schedule(block_mask, N_Q, N_KV, block_m, block_n, bool(is_causal),
+                                     int(sink_size), int(window_size), q.dtype == torch.float32)
                 _lib.check(lib.gki_bsa_fwd(
                     q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), dtype,
                     B, H, N_Q, N_KV, D, sched.lists.row_ptr.data_ptr(),
@@ -154,7 +155,8 @@ class _BlockSparseFlashAttention(torch.autograd.Function):
         delta = torch.empty((B, H, N_Q), dtype=torch.float32, device=q.device)
         with torch.cuda.device(q.device):
             stream = torch.cuda.current_stream(q.device).cuda_stream
-            sched = prefill_schedule(block_mask, N_Q, N_KV, ctx.block_m, ctx.block_n)
+            sched = bwd_schedule(block_mask, N_Q, N_KV, ctx.block_m, ctx.block_n, ctx.is_causal,
+                                 ctx.sink_size, ctx.window_size)
             L = sched.lists
             _lib.check(lib.gki_bsa_bwd(
                 q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(),

@@ -33,11 +33,12 @@ int gki_abi_version(void);
 /* Message of the last failing call on this thread. */
 const char* gki_last_error(void);
 
-/* Kernel tile geometry the schedules must be built for: prefill/backward tile
- * (tile_m x tile_n), decode q tile rows, and max query rows handled by the
+/* Kernel tile geometry the schedules must be built for: q rows of the forward
+ * tile for 16-bit and fp32 inputs, q rows of the backward tile, kv rows of
+ * every tile, q rows of the decode tile, and max query rows handled by the
  * decode kernel. Any pointer may be NULL. */
-int gki_tile_sizes(int32_t* tile_m, int32_t* tile_n, int32_t* decode_tile_m,
-                   int32_t* decode_max_q);
+int gki_tile_sizes(int32_t* fwd_tile_m_16, int32_t* fwd_tile_m_32, int32_t* bwd_tile_m,
+                   int32_t* tile_n, int32_t* decode_tile_m, int32_t* decode_max_q);
 
 /* Block-level StreamingLLM mask, bit-exact with `make_streaming_mask`
  * (sparse_triton_kernel.py:104-181): keep (i, j) iff q_hi > k_lo and
@@ -52,12 +53,16 @@ int gki_dense_mask(int32_t* mask, int64_t n_q, int64_t n_kv, int64_t block_m,
                    int64_t block_n, int32_t causal, void* stream);
 
 /* Classify the kernels' tile_m x tile_n tiles against a block mask of any
- * granularity: 0 = no kept block overlaps, 1 = all overlapping blocks kept,
- * 2 = partly kept. No reference counterpart: the reference gates its Triton
- * tiles directly on the mask (sparse_triton_kernel.py:283-285). */
+ * granularity, honouring the StreamingLLM token rule when is_causal:
+ * 0 = no in-bounds element is both kept by the lifted mask and allowed by the
+ * token rule, 1 = the lifted mask keeps every element the token rule allows,
+ * 2 = partly kept (kernels then consult the mask per element). No reference
+ * counterpart: the reference gates its Triton tiles directly on the mask
+ * (sparse_triton_kernel.py:283-285) and masks tokens inside (:312-322). */
 int gki_tile_mask(const int32_t* mask, int32_t n_qb, int32_t n_kb, int32_t block_m,
                   int32_t block_n, int32_t n_q, int32_t n_kv, int32_t tile_m,
-                  int32_t tile_n, int32_t* tile_mask, void* stream);
+                  int32_t tile_n, int32_t is_causal, int32_t sink_size,
+                  int32_t window_size, int32_t* tile_mask, void* stream);
 
 /* Kept-block list, step 1: per-row / per-column kept counts of an int32
  * [n_rows, n_cols] matrix and their exclusive prefix sums (row_ptr[n_rows+1],
@@ -83,7 +88,8 @@ int gki_heavy_order(const int32_t* col_ptr, int32_t n_cols, int32_t* order,
 /* Prefill forward: replaces the `_fwd_kernel` launch in
  * `_BlockSparseFlashAttention.forward` (sparse_triton_kernel.py:662-682).
  * O = softmax(mask(Q K^T * scale)) V, LSE = m + ln(l) (0 for empty rows).
- * row_ptr/row_idx: CSR over ceil(n_q/tile_m) q tiles of kept kv tiles. */
+ * row_ptr/row_idx: CSR over ceil(n_q/fwd_tile_m) q tiles (fwd_tile_m_16 or
+ * fwd_tile_m_32 by dtype) of kept kv tiles. */
 int gki_bsa_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
                 int32_t dtype, int32_t B, int32_t H, int32_t n_q, int32_t n_kv,
                 int32_t head_dim, const int32_t* row_ptr, const int32_t* row_idx,
@@ -94,7 +100,8 @@ int gki_bsa_fwd(const void* q, const void* k, const void* v, void* o, float* lse
 /* Backward: replaces the three launches in `_BlockSparseFlashAttention.backward`
  * (sparse_triton_kernel.py:719-777): Delta = rowsum(O * dO) into `delta`, then
  * dK/dV over the CSC list (kv_order / n_heavy from gki_heavy_order), then dQ
- * over the CSR list. dq, dk, dv are fully written (no zero-fill needed). */
+ * over the CSR list, both over bwd_tile_m x tile_n tiles. dq, dk, dv are fully
+ * written (no zero-fill needed). */
 int gki_bsa_bwd(const void* q, const void* k, const void* v, const void* o,
                 const void* dout, const float* lse, void* dq, void* dk, void* dv,
                 float* delta, int32_t dtype, int32_t B, int32_t H, int32_t n_q,

@@ -17,8 +17,9 @@ How each is pinned (by the tests in ``tests/test_oracle_pins.py``):
   restated) on the reference's 13 shapes.
 * ``dense_block_mask``    -- sparse_triton_kernel.py:184-210. Pinned by brute force.
 * ``kept_lists``          -- build-only (CSR/CSC). Pinned by ``np.nonzero``.
-* ``tile_classes``        -- build-only tile classification. Pinned by brute
-  force over the lifted token mask.
+* ``tile_classes``        -- build-only tile classification. Pinned per tile
+  against ``effective_mask`` (visited iff some effective element; class 1 iff
+  the effective mask equals the token rule there).
 * ``attention_fwd/bwd``   -- sparse_triton_kernel.py:845-902 (eager oracle) with
   the kernel's LSE sentinel (:341-352). Pinned against a pure-Python loop on
   tiny inputs, torch's math SDPA with an explicit mask, torch autograd
@@ -117,17 +118,22 @@ def kept_lists(m: np.ndarray) -> Tuple[np.ndarray, np.ndarray, np.ndarray, np.nd
     return row_ptr, row_idx, col_ptr, col_idx
 
 
-def tile_classes(mask: np.ndarray, n_q: int, n_kv: int, bm: int, bn: int, tm: int,
-                 tn: int) -> np.ndarray:
-    """0 = tile has no kept token of lift(mask); 1 = every in-bounds token of the
-    tile is kept by lift(mask); 2 = some but not all."""
+def tile_classes(mask: np.ndarray, n_q: int, n_kv: int, bm: int, bn: int, tm: int, tn: int,
+                 causal: bool = False, sink: int = 0, window: int = 0) -> np.ndarray:
+    """Per tm x tn tile of the kernels: 0 = no in-bounds element is visible
+    (kept by lift(mask) and, when causal, allowed by the token rule); 1 = the
+    lifted mask keeps every element the token rule allows (all elements when
+    not causal), so the kernel needs only the token rule; 2 = otherwise."""
     lifted = lift(mask, bm, bn, n_q, n_kv)
+    tok = token_mask(n_q, n_kv, sink, window) if causal else np.ones((n_q, n_kv), bool)
     n_qt, n_kt = -(-n_q // tm), -(-n_kv // tn)
     out = np.zeros((n_qt, n_kt), np.int32)
     for a in range(n_qt):
         for b in range(n_kt):
-            blk = lifted[a * tm:(a + 1) * tm, b * tn:(b + 1) * tn]
-            out[a, b] = 0 if not blk.any() else (1 if blk.all() else 2)
+            sl = (slice(a * tm, (a + 1) * tm), slice(b * tn, (b + 1) * tn))
+            allowed, kept = tok[sl], lifted[sl]
+            if (allowed & kept).any():
+                out[a, b] = 2 if (allowed & ~kept).any() else 1
     return out
 
 

@@ -19,8 +19,8 @@ import torch
 
 import fx_compiler_pass as fxp
 import sparse_triton_kernel as stk
-from gki import build_block_lists
-from gki.lists import decode_schedule, prefill_schedule
+from gki import _lib, build_block_lists
+from gki.lists import bwd_schedule, decode_schedule, fwd_schedule
 from oracle import chunked_reference as cr
 from oracle import streaming_oracle as so
 
@@ -98,13 +98,18 @@ def test_kept_block_lists_random_and_empty():
             np.testing.assert_array_equal(got.cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("n_q,n_kv,sink,window,bm,bn",
                          [(300, 300, 4, 64, 16, 16), (1000, 1000, 4, 128, 128, 32),
                           (8192, 8192, 4, 1024, 64, 64), (200, 333, 2, 50, 8, 128)])
-def test_prefill_schedule_matches_oracle(n_q, n_kv, sink, window, bm, bn):
+def test_schedules_match_oracle(n_q, n_kv, sink, window, bm, bn, causal):
     m = so.block_mask(n_q, n_kv, sink, window, bm, bn)
-    sched = prefill_schedule(torch.from_numpy(m).to(DEV), n_q, n_kv, bm, bn)
-    tiles = so.tile_classes(m, n_q, n_kv, bm, bn, 64, 64)
+    dm = torch.from_numpy(m).to(DEV)
+    ts = _lib.tile_sizes()
+    # backward: CSR + CSC over 64x64 tiles, heavy-first column order
+    sched = bwd_schedule(dm, n_q, n_kv, bm, bn, causal, sink, window)
+    tiles = so.tile_classes(m, n_q, n_kv, bm, bn, ts["bwd_tile_m"], ts["tile_n"], causal, sink,
+                            window)
     ref = so.kept_lists(tiles)
     L = sched.lists
     for got, want in zip((L.row_ptr, L.row_idx, L.col_ptr, L.col_idx), ref):
@@ -112,6 +117,14 @@ def test_prefill_schedule_matches_oracle(n_q, n_kv, sink, window, bm, bn):
     order, n_heavy = so.heavy_order(ref[2])
     np.testing.assert_array_equal(sched.kv_order.cpu().numpy(), order)
     assert sched.n_heavy == n_heavy
+    # forward: CSR over the per-dtype q tiles
+    for fp32, key in ((False, "fwd_tile_m_16"), (True, "fwd_tile_m_32")):
+        fs = fwd_schedule(dm, n_q, n_kv, bm, bn, causal, sink, window, fp32)
+        tiles = so.tile_classes(m, n_q, n_kv, bm, bn, ts[key], ts["tile_n"], causal, sink, window)
+        ref = so.kept_lists(tiles)
+        assert fs.n_qt == tiles.shape[0]
+        np.testing.assert_array_equal(fs.lists.row_ptr.cpu().numpy(), ref[0])
+        np.testing.assert_array_equal(fs.lists.row_idx.cpu().numpy(), ref[1])
 
 
 def test_decode_schedule_matches_oracle():

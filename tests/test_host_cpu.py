@@ -99,7 +99,8 @@ def test_library_exports_every_declared_symbol():
 
 def test_tile_sizes():
     ts = _lib.tile_sizes()
-    assert ts == {"tile_m": 64, "tile_n": 64, "decode_tile_m": 16, "decode_max_q": 4}
+    assert ts == {"fwd_tile_m_16": 128, "fwd_tile_m_32": 64, "bwd_tile_m": 64, "tile_n": 64,
+                  "decode_tile_m": 16, "decode_max_q": 4}
 
 
 def test_capi_rejects_bad_arguments_before_launch():

@@ -174,6 +174,36 @@ def test_tile_classes_aligned_and_unaligned():
     assert (t16 == 2).any()
 
 
+@pytest.mark.parametrize("n_q,n_kv,sink,window,bm,bn,tm,tn",
+                         [(300, 300, 4, 64, 16, 16, 64, 64), (300, 300, 4, 64, 16, 16, 128, 64),
+                          (200, 333, 2, 50, 8, 128, 128, 64), (130, 260, 0, 1, 32, 32, 64, 64),
+                          (1, 700, 4, 100, 1, 64, 16, 64), (257, 257, 3, 0, 64, 64, 128, 64),
+                          (300, 300, 4, 64, 64, 64, 64, 64)])
+def test_tile_classes_causal_against_effective_mask(n_q, n_kv, sink, window, bm, bn, tm, tn):
+    """Each tile's class follows from the effective (kernel-visible) mask:
+    visited iff some element is visible; class 1 iff, inside the tile, the
+    effective mask equals the token rule alone (so the kernel may skip the
+    mask lookup); class 2 otherwise. A random mask with holes exercises 2."""
+    rng = np.random.default_rng(n_q * 7 + n_kv)
+    m = so.block_mask(n_q, n_kv, sink, window, bm, bn)
+    m_holes = m * (rng.random(m.shape) < 0.7)
+    for mm in (m, m_holes):
+        t = so.tile_classes(mm, n_q, n_kv, bm, bn, tm, tn, True, sink, window)
+        eff = so.effective_mask(mm, n_q, n_kv, bm, bn, True, sink, window)
+        tok = np.array([[so.visible(n_kv - n_q + i, j, sink, window) for j in range(n_kv)]
+                        for i in range(n_q)])
+        for a, b in itertools.product(range(t.shape[0]), range(t.shape[1])):
+            sl = (slice(tm * a, tm * a + tm), slice(tn * b, tn * b + tn))
+            if not eff[sl].any():
+                assert t[a, b] == 0
+            else:
+                assert t[a, b] == (1 if (eff[sl] == tok[sl]).all() else 2)
+        # the streaming mask itself never needs a per-element lookup when the
+        # tile and block grids coincide
+        if mm is m and (bm, bn) == (tm, tn):
+            assert not (t == 2).any()
+
+
 def test_heavy_order_puts_sink_column_first():
     m = so.block_mask(8192, 8192, 4, 1024, 64, 64)
     _, _, col_ptr, _ = so.kept_lists(m)
