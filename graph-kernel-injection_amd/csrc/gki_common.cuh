@@ -42,6 +42,8 @@ struct F16 {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
                                                    __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
   }
+  // eight 1.0 elements: an all-ones MFMA operand (row sums on the matrix pipe)
+  __device__ static inline uint4 ones8() { return make_uint4(0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u); }
 };
 struct BF16 {
   using storage = uint16_t;
@@ -57,6 +59,7 @@ struct BF16 {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
                                                     __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   }
+  __device__ static inline uint4 ones8() { return make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u); }
 };
 
 __device__ inline floatx4 mfma_f32(float a, float b, floatx4 c) {
@@ -99,15 +102,31 @@ __device__ inline uint4 pack8(const floatx4& lo, const floatx4& hi) {
 }
 
 // LDS tile layout for 16-bit [64][D] tiles: row-major, no padding, 16-byte
-// chunks XOR-swizzled per row by swz(row) = 2*(row&3) + ((row>>3)&1) (kept
-// below the chunk count). Conflict-free for both access patterns the kernels
-// use: 16-byte reads of rows {b..b+3, b+8..b+11} at one chunk (the rho() row
-// order), and ds_read_b64_tr_b16 over 4 consecutive rows x 2 adjacent chunks.
+// chunks XOR-swizzled per row. gfx950 LDS has 64 banks of 4 bytes (one
+// 256-byte "bank row" per clock), so a read is conflict-free when the 16-byte
+// chunks that one clock serves land on 16 distinct positions of a bank row.
+// With a = row & 3, b = (row >> 3) & 3 the swizzle is a bijection of the
+// (a, b) pairs the two read patterns touch at once:
+//  * 16-byte reads of rows {b..b+3, b+8..b+11, b+16.., b+24..} at one chunk
+//    (the rho() row order; 16 lanes per clock),
+//  * ds_read_b64_tr_b16 over rows {r..r+3, r+8..r+11} x 2 adjacent chunks
+//    (32 lanes per clock),
+// and the tile fill (consecutive lanes, consecutive chunks of one bank row).
+// Tiles narrower than 256 bytes share a bank row between 256/(2D) rows; the
+// row bits that select the slice take the place of a. D = 16 keeps a 2-way
+// conflict (only 2 chunks per row).
+template <int D>
+__device__ inline int lds_swz(int row) {
+  const int b = (row >> 3) & 3;
+  const int bb = 2 * (b & 1) + (b >> 1);
+  if constexpr (D >= 128) return (4 * (row & 3) + bb) & (D / 8 - 1);
+  else if constexpr (D == 64) return 4 * ((row >> 1) & 1) + bb;
+  else if constexpr (D == 32) return bb;
+  else return 0;
+}
 template <int D>
 __device__ inline int lds_off(int row, int col) {
-  constexpr int CPR = D / 8;
-  const int sw = (2 * (row & 3) + ((row >> 3) & 1)) & (CPR - 1);
-  return row * D + ((((col >> 3) ^ sw)) << 3) + (col & 7);
+  return row * D + ((((col >> 3) ^ lds_swz<D>(row))) << 3) + (col & 7);
 }
 
 // Transposed MFMA operand from a swizzled 16-bit LDS tile via
@@ -164,6 +183,64 @@ struct RowTile {
     for (int p = 0; p < P; ++p) {
       const int c = tid + 256 * p;
       if (c < CH) *(uint4*)(lds + lds_off<D>(c / CPR, (c % CPR) * 8)) = reg[p];
+    }
+  }
+};
+
+// LDS byte address of a pointer into __shared__ memory.
+__device__ inline uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+
+// One gfx950 LDS-DMA load: every lane fetches 16 bytes from its global address
+// `src` and the wave writes them to LDS bytes [lds, lds + 1024), lane i at
+// lds + 16 i. Issued as inline asm so that the compiler does not guard every
+// later LDS read with a wait on it (it cannot tell which buffer the DMA
+// targets); callers wait explicitly with dma_wait() before the barrier that
+// publishes the buffer. Only M0 and memory are touched.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ inline void dma_load16(const void* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+// Wait until this wave's vector-memory operations (LDS-DMA included) are done:
+// s_waitcnt vmcnt(0) (gfx9 encoding: vmcnt 0, expcnt 7, lgkmcnt 15). Issued via
+// the builtin so the compiler's own wait tracking also sees every earlier load
+// as complete and inserts no further vmcnt waits for them.
+__device__ inline void dma_wait() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Stage a full 64-row tile of a row-major [n, D] 16-bit matrix straight into
+// the swizzled LDS layout with LDS-DMA loads: no VGPR staging and no ds_write.
+// One wave instruction fills 1 KB of LDS, lane i writing bytes 16i..16i+15,
+// so the swizzle is applied on the global side: lane i fetches the chunk that
+// belongs at its LDS position. The 256 threads cover the tile's D/8 blocks of
+// 1 KB; `off` is the lane's element offset inside the tile for each block it
+// moves (computed once). Only for tiles whose 64 rows are all in bounds.
+template <int D>
+struct DmaTile {
+  static constexpr int NB = D / 8;                     // 1 KB blocks per tile
+  static constexpr int NP = (NB + 3) / 4;              // blocks per wave
+  int off[NP];
+  int wave;
+  __device__ inline void init(int tid) {
+    wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const int e = (4 * p + wave) * 512 + 8 * lane;   // LDS element offset
+      const int row = e / D, pch = (e % D) >> 3;
+      off[p] = row * D + ((pch ^ lds_swz<D>(row)) << 3);
+    }
+  }
+  __device__ inline void load(const uint16_t* base, int r0, const uint16_t* lds) const {
+    const uint16_t* src = base + (size_t)r0 * D;
+    const uint32_t l0 = lds_addr(lds);
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const int blk = 4 * p + wave;
+      if (NB % 4 == 0 || blk < NB) dma_load16(src + off[p], l0 + blk * 1024);
     }
   }
 };

@@ -28,6 +28,12 @@
 namespace gki {
 namespace {
 
+// Online-softmax reference max moves only when a tile's row max exceeds it by
+// more than this many log2 units, so p = exp2(s - m) stays below 2^8 and the O
+// rescale is almost never needed. O = acc / l and LSE = m + ln(l) are exact for
+// any reference max.
+constexpr float kRescaleSlack = 8.f;
+
 template <typename T, int D>
 __global__ __launch_bounds__(256, 2) void fwd_kernel_16(
     Geom g, const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
@@ -35,7 +41,6 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel_16(
     const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ row_idx, int n_qt) {
   constexpr int KS = (D + 31) / 32;   // k-steps of the QK^T contraction
   constexpr int DT = D / 16;          // 16-row tiles of O^T
-  using Tile = RowTile<D>;
   __shared__ __align__(16) uint16_t sk[2][kTileN * D];
   __shared__ __align__(16) uint16_t sv[2][kTileN * D];
 
@@ -65,17 +70,32 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel_16(
   for (int h = 0; h < 2; ++h)
 #pragma unroll
     for (int i = 0; i < DT; ++i) o[h][i] = floatx4{0.f, 0.f, 0.f, 0.f};
-  float m[2] = {kNegInf, kNegInf}, l[2] = {0.f, 0.f};
+  // Row sums run on the MFMA pipe (ones x P^T): lane (g, c) holds the sum of
+  // row c in every component; it sums the same 16-bit P that multiplies V.
+  floatx4 lsum[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
+  float m[2] = {kNegInf, kNegInf};
+  const uint4 ones = T::ones8();
+
+  DmaTile<D> dma;
+  dma.init(tid);
+  // Full tiles go LDS-DMA; the ragged last kv tile goes through registers so
+  // that its out-of-range rows are zero (P = 0 must not meet stale V).
+  auto stage = [&](int k0, int b) {
+    if (k0 + kTileN <= g.n_kv) {
+      dma.load(K + kb, k0, sk[b]);
+      dma.load(V + kb, k0, sv[b]);
+    } else {
+      RowTile<D> t;
+      t.load(K + kb, k0, g.n_kv, tid);
+      t.store(sk[b], tid);
+      t.load(V + kb, k0, g.n_kv, tid);
+      t.store(sv[b], tid);
+    }
+  };
 
   const int e_beg = row_ptr[qt], e_end = row_ptr[qt + 1];
-  Tile tk, tv;
-  if (e_beg < e_end) {
-    const int k0 = (row_idx[e_beg] & kIdxMask) * kTileN;
-    tk.load(K + kb, k0, g.n_kv, tid);
-    tv.load(V + kb, k0, g.n_kv, tid);
-    tk.store(sk[0], tid);
-    tv.store(sv[0], tid);
-  }
+  if (e_beg < e_end) stage((row_idx[e_beg] & kIdxMask) * kTileN, 0);
+  dma_wait();
   __syncthreads();
 
   for (int e = e_beg; e < e_end; ++e) {
@@ -83,12 +103,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel_16(
     const int ent = row_idx[e];
     const int k0 = (ent & kIdxMask) * kTileN;
     const bool partial = (ent >> kPartialBit) & 1;
-    const bool has_next = e + 1 < e_end;
-    if (has_next) {
-      const int k1 = (row_idx[e + 1] & kIdxMask) * kTileN;
-      tk.load(K + kb, k1, g.n_kv, tid);
-      tv.load(V + kb, k1, g.n_kv, tid);
-    }
+    if (e + 1 < e_end) stage((row_idx[e + 1] & kIdxMask) * kTileN, buf ^ 1);
     const uint16_t* ck = sk[buf];
     const uint16_t* cv = sv[buf];
 
@@ -125,26 +140,20 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel_16(
 #pragma unroll
         for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[h][t][i]);
       mx = wave_max16x4(mx) * g.scale_log2;     // softmax_scale > 0 (checked on the host)
-      const float m_new = fmaxf(m[h], mx);
-      const float m_use = (m_new == kNegInf) ? 0.f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m[h] - m_use);
-      float rs = 0.f;
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[h][t][i], g.scale_log2, -m_use));
-          s[h][t][i] = p;
-          rs += p;
-        }
-      }
-      l[h] = l[h] * alpha + rs;
-      m[h] = m_new;
-      // alpha == 1 exactly when no row max of the block moved: skipping is exact
-      if (__any(alpha != 1.f)) {
+      const bool grow = mx > m[h] + kRescaleSlack;
+      if (__any(grow)) {
+        const float alpha = grow ? __builtin_amdgcn_exp2f(m[h] - mx) : 1.f;
+        m[h] = grow ? mx : m[h];
+        lsum[h][0] *= alpha;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) o[h][dt] *= alpha;
       }
+      const float m_use = (m[h] == kNegInf) ? 0.f : m[h];
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          s[h][t][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[h][t][i], g.scale_log2, -m_use));
     }
 
 #pragma unroll
@@ -157,18 +166,17 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel_16(
         o[0][dt] = T::mfma(a, b0, o[0][dt]);
         o[1][dt] = T::mfma(a, b1, o[1][dt]);
       }
+      lsum[0] = T::mfma(ones, b0, lsum[0]);
+      lsum[1] = T::mfma(ones, b1, lsum[1]);
     }
-    if (has_next) {
-      tk.store(sk[buf ^ 1], tid);
-      tv.store(sv[buf ^ 1], tid);
-    }
+    dma_wait();        // the next tile's LDS-DMA has landed before the barrier
     __syncthreads();
   }
 
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int my_q = qw + 16 * h + col;
-    const float l_tot = wave_sum16x4(l[h]);
+    const float l_tot = lsum[h][0];
     const bool valid = l_tot > 0.f;
     const float inv = valid ? 1.f / l_tot : 1.f;
     if (my_q < g.n_q) {
