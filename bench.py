@@ -55,23 +55,30 @@ def _randn(shape, gen, scale, dtype, device):
 
 
 def _time_calls(fn, steps: int, warmup: int):
-    """Warm up, then time ``steps`` calls; returns (per-call ms list, total ms)."""
+    """Warm up, then time ``steps`` back-to-back calls between one pair of HIP
+    events (the throughput a caller's loop sees, launch gaps included), then a
+    second pass with events around every call for the per-call distribution.
+    Returns (ms per step from the first pass, per-call ms list)."""
     import torch
 
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(steps):
+        fn()
+    t1.record()
+    torch.cuda.synchronize()
+    per_step = t0.elapsed_time(t1) / steps
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(steps)]
-    t_all0, t_all1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t_all0.record()
     for a, b in evs:
         a.record()
         fn()
         b.record()
-    t_all1.record()
     torch.cuda.synchronize()
-    return [a.elapsed_time(b) for a, b in evs], t_all0.elapsed_time(t_all1)
+    return per_step, [a.elapsed_time(b) for a, b in evs]
 
 
 def _roofline(achieved: float, peak: float, unit: str, bound: str, traffic=None) -> dict:
@@ -97,18 +104,17 @@ def section_c2(steps: int, warmup: int, keep_cpu_inputs: bool):
         return stk.block_sparse_attention(q, k, v, mask, block_m=bm, block_n=bm, is_causal=True,
                                           sink_size=S, window_size=W)
 
-    per, total = _time_calls(fn, steps, warmup)
-    avg = statistics.mean(per)
+    avg, per = _time_calls(fn, steps, warmup)
     tflops = flops / (avg * 1e-3) / 1e12
-    log(f"[c2] fwd kernel avg {avg:.4f} ms (p50 {statistics.median(per):.4f}), "
-        f"{tflops:.1f} TFLOP/s, step {total / steps:.4f} ms")
+    log(f"[c2] fwd step {avg:.4f} ms back-to-back (per call p50 {statistics.median(per):.4f}), "
+        f"{tflops:.1f} TFLOP/s")
     cpu_inputs = None
     if keep_cpu_inputs:
         cpu_inputs = tuple(t.to(torch.bfloat16).float() for t in (q32, k32, v32)) + (mask.cpu(),)
     del q, k, v
     return {
         "kept_tiles": kept, "flops_per_step": flops, "avg_ms": avg, "p50_ms": statistics.median(per),
-        "ms_per_step": total / steps, "tflops": tflops,
+        "ms_per_step": avg, "tflops": tflops,
     }, cpu_inputs
 
 
@@ -182,13 +188,12 @@ def section_c4(steps: int, warmup: int) -> dict:
         return stk.block_sparse_attention(q, k, v, mask, block_m=1, block_n=64, is_causal=True,
                                           sink_size=S, window_size=W)
 
-    per, total = _time_calls(fn, steps, warmup)
-    avg = statistics.mean(per)
+    avg, per = _time_calls(fn, steps, warmup)
     gbs = exact_bytes / (avg * 1e-3) / 1e9
     res = {
         "workload": "c4 decode step: B8 H32 n_q=1 KV100000 D128 bf16, S4 W2048, BM=1 BN=64",
         "kept_tiles": kept, "kv_bytes_token_exact": exact_bytes, "kv_bytes_block_granular": block_bytes,
-        "avg_ms": avg, "p50_ms": statistics.median(per), "ms_per_step": total / steps,
+        "avg_ms": avg, "p50_ms": statistics.median(per), "ms_per_step": avg,
         "kv_gbs": gbs, "kv_gbs_block_granular": block_bytes / (avg * 1e-3) / 1e9,
     }
     res["roofline"] = _roofline(gbs, PEAK_HBM, "GB/s", "hbm")
@@ -321,7 +326,8 @@ def main() -> int:
         line["train"] = section_c3(args.steps, args.warmup)
         torch.cuda.empty_cache()
     if "c4" in sections:
-        line["decode"] = section_c4(args.steps, args.warmup)
+        # a decode step is ~45 us: time more of them for a stable mean
+        line["decode"] = section_c4(max(args.steps, 200), max(args.warmup, 20))
         torch.cuda.empty_cache()
     if "c5" in sections:
         line["layer_c5"] = section_c5(max(3, args.steps // 4), 2)

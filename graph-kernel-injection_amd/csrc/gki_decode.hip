@@ -10,11 +10,12 @@
 //     query row can see (the hull of sink prefix / window suffix / in-bounds
 //     rows of each tile): S + W positions per head for n_q = 1;
 //   * decode_kernel: workgroup (bh, split) takes an equal slice of that stream
-//     and each of its 16 waves streams a contiguous 1/16 of the slice in
-//     rounds of 8 token-row passes: all 16-byte K and V loads of a round are
-//     issued together (D/8 lanes per row, non-temporal), then scores, a
-//     wave-local online softmax and P V. No barrier until the end, where the
-//     waves merge in LDS. With one split per head the workgroup writes O and
+//     and each of its 12 waves streams a contiguous 1/12 of the slice in
+//     rounds of 4 token-row passes (16-byte non-temporal K and V loads, D/8
+//     lanes per row), double-buffered: the next round's loads are issued
+//     before the current one is consumed (scores, wave-local online softmax,
+//     P V), so every CU keeps HBM busy through its compute. No barrier until
+//     the end, where the waves merge in LDS. With one split per head the workgroup writes O and
 //     LSE itself; otherwise it writes (acc[D], m, l) to a workspace and
 //   * combine_kernel (one wave per row) merges the splits:
 //     O = sum acc_s 2^(m_s-M) / sum l_s 2^(m_s-M), LSE = M ln2 + ln L,
@@ -92,7 +93,98 @@ __global__ __launch_bounds__(256) void decode_tokens_kernel(Geom g, const int32_
   if (threadIdx.x == 0) *count = carry;
 }
 
-constexpr int kDecodeWaves = 16;   // one 1024-thread workgroup per (b, h, split)
+constexpr int kDecodeWaves = 12;   // one 768-thread workgroup per (b, h, split): 3 waves per SIMD
+
+// One round of a wave: NU passes of TPW token rows, LPT lanes per row, one
+// 16-byte K and V chunk per lane and pass.
+template <typename T, int D, int NU>
+struct DecodeRound {
+  using S = typename T::storage;
+  static constexpr int VEC = 16 / sizeof(S);
+  static constexpr int LPT = D / VEC;
+  static constexpr int TPW = 64 / LPT;
+  static constexpr int RT = NU * TPW;
+  int pj[NU];
+  uint4 kr[NU], vr[NU];
+  // Token positions of round t0 for this lane's row (one dword load per pass).
+  // Rows past the wave's slice read the slice's last entry, flagged by the
+  // sign bit: every load stays in range and unconditional (no branch, so no
+  // wait is forced on the loads in flight) and the row is masked when consumed.
+  __device__ static inline void positions(const int32_t* __restrict__ tok, int t0, int w1, int tk,
+                                          int (&pos)[NU]) {
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      const int t = t0 + u * TPW + tk;
+      const int v = tok[t < w1 ? t : w1 - 1];
+      pos[u] = t < w1 ? v : (v | (1 << 31));
+    }
+  }
+  __device__ inline void fetch(const int (&pos)[NU], int ch, const S* __restrict__ K,
+                               const S* __restrict__ V, size_t kb) {
+#pragma unroll
+    for (int u = 0; u < NU; ++u) pj[u] = pos[u];
+#pragma unroll
+    for (int u = 0; u < NU; ++u) kr[u] = ld_nt16(K + kb + (size_t)(pj[u] & kIdxMask) * D + ch * VEC);
+#pragma unroll
+    for (int u = 0; u < NU; ++u) vr[u] = ld_nt16(V + kb + (size_t)(pj[u] & kIdxMask) * D + ch * VEC);
+  }
+};
+
+template <typename T, int D, int NQ, int NU>
+__device__ inline void decode_consume(const Geom& g, const DecodeRound<T, D, NU>& rd,
+                                      const float (&qv)[NQ][16 / sizeof(typename T::storage)],
+                                      float (&m)[NQ], float (&l)[NQ],
+                                      float (&acc)[NQ][16 / sizeof(typename T::storage)]) {
+  using S = typename T::storage;
+  using R = DecodeRound<T, D, NU>;
+  constexpr int VEC = R::VEC, LPT = R::LPT;
+  float sc[NQ][NU];
+#pragma unroll
+  for (int u = 0; u < NU; ++u) {
+    const S* e = (const S*)&rd.kr[u];
+    float kf[VEC];
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) kf[i] = T::to_float(e[i]);
+#pragma unroll
+    for (int r = 0; r < NQ; ++r) {
+      float part = 0.f;
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) part += qv[r][i] * kf[i];
+#pragma unroll
+      for (int off = LPT / 2; off > 0; off >>= 1) part += __shfl_xor(part, off);
+      bool ok = rd.pj[u] >= 0 && r < g.n_q;    // sign bit: padding row of the round
+      if (ok) ok = elem_valid(g, r, rd.pj[u] & kIdxMask, (rd.pj[u] >> kPartialBit) & 1);
+      sc[r][u] = ok ? part * g.scale_log2 : kNegInf;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < NQ; ++r) {
+    float mx = kNegInf;
+#pragma unroll
+    for (int u = 0; u < NU; ++u) mx = fmaxf(mx, sc[r][u]);
+#pragma unroll
+    for (int off = LPT; off < 64; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    const float m_new = fmaxf(m[r], mx);
+    const float mu = m_new == kNegInf ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m[r] - mu);
+    m[r] = m_new;
+    float rs = 0.f;
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) acc[r][i] *= alpha;
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      const float p = __builtin_amdgcn_exp2f(sc[r][u] - mu);
+      rs += p;
+      const float pv = T::is_f32 ? p : T::to_float(T::from_float(p));   // P -> V dtype
+      // a padding row re-reads a real V row: zero it so 0 * inf cannot appear
+      const uint4 vz = rd.pj[u] >= 0 ? rd.vr[u] : make_uint4(0, 0, 0, 0);
+      const S* e = (const S*)&vz;
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) acc[r][i] += pv * T::to_float(e[i]);
+    }
+    l[r] = l[r] * alpha + rs;
+  }
+}
 
 template <typename T, int D, int NQ>
 __global__ __launch_bounds__(64 * kDecodeWaves) void decode_kernel(
@@ -101,16 +193,15 @@ __global__ __launch_bounds__(64 * kDecodeWaves) void decode_kernel(
     float* __restrict__ LSE, float* __restrict__ ws, const int32_t* __restrict__ tok, int n_tokens,
     int n_splits) {
   using S = typename T::storage;
-  constexpr int VEC = 16 / sizeof(S);
-  constexpr int LPT = D / VEC;      // lanes per token row
-  constexpr int TPW = 64 / LPT;     // token rows per wave pass
-  constexpr int NU = 8;             // passes per round (16-byte K and V loads in flight per lane)
-  constexpr int RT = NU * TPW;      // tokens per wave round
+  constexpr int NU = NQ == 1 ? 4 : 2;   // passes per round; two rounds in flight (double-buffered)
+  using R = DecodeRound<T, D, NU>;
+  constexpr int VEC = R::VEC, LPT = R::LPT, RT = R::RT;
   constexpr int NW = kDecodeWaves;
   __shared__ float wm[NW][NQ], wl[NW][NQ];
   __shared__ float wacc[NW][NQ][D];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int split = blockIdx.x % n_splits, bh = blockIdx.x / n_splits;
   const size_t qb = (size_t)bh * g.n_q * D;
   const size_t kb = (size_t)bh * g.n_kv * D;
@@ -141,64 +232,29 @@ __global__ __launch_bounds__(64 * kDecodeWaves) void decode_kernel(
     for (int i = 0; i < VEC; ++i) acc[r][i] = 0.f;
   }
 
-  for (int t0 = w0; t0 < w1; t0 += RT) {
-    int pj[NU];
-#pragma unroll
-    for (int u = 0; u < NU; ++u) {
-      const int t = t0 + u * TPW + tk;
-      pj[u] = t < w1 ? tok[t] : -1;
-    }
-    uint4 kr[NU], vr[NU];
-#pragma unroll
-    for (int u = 0; u < NU; ++u)
-      kr[u] = pj[u] >= 0 ? ld_nt16(K + kb + (size_t)(pj[u] & kIdxMask) * D + ch * VEC) : make_uint4(0, 0, 0, 0);
-#pragma unroll
-    for (int u = 0; u < NU; ++u)
-      vr[u] = pj[u] >= 0 ? ld_nt16(V + kb + (size_t)(pj[u] & kIdxMask) * D + ch * VEC) : make_uint4(0, 0, 0, 0);
-
-    float sc[NQ][NU];
-#pragma unroll
-    for (int u = 0; u < NU; ++u) {
-      const S* e = (const S*)&kr[u];
-      float kf[VEC];
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) kf[i] = T::to_float(e[i]);
-#pragma unroll
-      for (int r = 0; r < NQ; ++r) {
-        float part = 0.f;
-#pragma unroll
-        for (int i = 0; i < VEC; ++i) part += qv[r][i] * kf[i];
-#pragma unroll
-        for (int off = LPT / 2; off > 0; off >>= 1) part += __shfl_xor(part, off);
-        bool ok = pj[u] >= 0 && r < g.n_q;
-        if (ok) ok = elem_valid(g, r, pj[u] & kIdxMask, (pj[u] >> kPartialBit) & 1);
-        sc[r][u] = ok ? part * g.scale_log2 : kNegInf;
+  // Rounds alternate between two register sets: the K / V loads of round i+1
+  // (and the positions of round i+2) are issued before round i is consumed, so
+  // HBM streams while the VALU works. Loads complete in order, so each wait
+  // covers only the oldest round.
+  if (w0 < w1) {
+    R ra, rb;
+    int pa[NU], pb[NU];
+    R::positions(tok, w0, w1, tk, pa);
+    R::positions(tok, w0 + RT, w1, tk, pb);
+    ra.fetch(pa, ch, K, V, kb);
+    for (int t0 = w0; t0 < w1; t0 += 2 * RT) {
+      const bool has_b = t0 + RT < w1;
+      if (has_b) {
+        R::positions(tok, t0 + 2 * RT, w1, tk, pa);
+        rb.fetch(pb, ch, K, V, kb);
       }
-    }
-#pragma unroll
-    for (int r = 0; r < NQ; ++r) {
-      float mx = kNegInf;
-#pragma unroll
-      for (int u = 0; u < NU; ++u) mx = fmaxf(mx, sc[r][u]);
-#pragma unroll
-      for (int off = LPT; off < 64; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-      const float m_new = fmaxf(m[r], mx);
-      const float mu = m_new == kNegInf ? 0.f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m[r] - mu);
-      m[r] = m_new;
-      float rs = 0.f;
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) acc[r][i] *= alpha;
-#pragma unroll
-      for (int u = 0; u < NU; ++u) {
-        const float p = __builtin_amdgcn_exp2f(sc[r][u] - mu);
-        rs += p;
-        const float pv = T::is_f32 ? p : T::to_float(T::from_float(p));   // P -> V dtype
-        const S* e = (const S*)&vr[u];
-#pragma unroll
-        for (int i = 0; i < VEC; ++i) acc[r][i] += pv * T::to_float(e[i]);
+      decode_consume<T, D, NQ, NU>(g, ra, qv, m, l, acc);
+      if (!has_b) break;
+      if (t0 + 2 * RT < w1) {
+        R::positions(tok, t0 + 3 * RT, w1, tk, pb);
+        ra.fetch(pa, ch, K, V, kb);
       }
-      l[r] = l[r] * alpha + rs;
+      decode_consume<T, D, NQ, NU>(g, rb, qv, m, l, acc);
     }
   }
   // merge the token-row groups of the wave (same m), then the four waves

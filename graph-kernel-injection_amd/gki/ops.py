@@ -26,7 +26,7 @@ from .lists import _CACHE, bwd_schedule, decode_schedule, fwd_schedule
 _DTYPE_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 _HEAD_DIMS = (16, 32, 64, 128)
 _DECODE_HEAD_DIMS = (64, 128)
-# decode workgroups to aim for: one 1024-thread group on each of the 256 CUs
+# decode workgroups to aim for: one 768-thread group on each of the 256 CUs
 _DECODE_TARGET_WGS = 256
 
 
@@ -41,8 +41,8 @@ def _device_mask(block_mask: torch.Tensor, device: torch.device) -> torch.Tensor
 
 
 def _decode_splits(n_tokens: int, bh: int) -> int:
-    """1024-thread workgroups per (b, h) for the decode step: about one per CU
-    in total, but at least ~1024 tokens (64 per wave) per workgroup."""
+    """Decode workgroups per (b, h): about one per CU in total, but at least
+    ~1024 tokens (about 85 per wave) per workgroup."""
     want = -(-_DECODE_TARGET_WGS // bh)
     cap = max(1, n_tokens // 1024)
     return max(1, min(want, cap))
