@@ -81,6 +81,19 @@ def _time_calls(fn, steps: int, warmup: int):
     return per_step, [a.elapsed_time(b) for a, b in evs]
 
 
+def _traffic(*keys: str):
+    """HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE (scaled
+    by a plain copy of known size), summed over the named kernels; from
+    profiles/hbm_traffic.json, which the profiling commands in
+    profiles/hbm_traffic_c2_c3_c4.md produce. None when not profiled."""
+    path = ROOT / "profiles" / "hbm_traffic.json"
+    try:
+        table = json.loads(path.read_text())["kernels"]
+        return int(sum(table[k]["hbm_bytes"] for k in keys))
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def _roofline(achieved: float, peak: float, unit: str, bound: str, traffic=None) -> dict:
     return {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
             "frac": round(achieved / peak, 4), "traffic": traffic}
@@ -162,7 +175,8 @@ def section_c3(steps: int, warmup: int) -> dict:
         "fwd_tflops": f_fwd / (fwd * 1e-3) / 1e12, "bwd_tflops": f_bwd / (bwd * 1e-3) / 1e12,
         "fwdbwd_tflops": (f_fwd + f_bwd) / ((fwd + bwd) * 1e-3) / 1e12,
     }
-    res["roofline"] = _roofline(res["fwdbwd_tflops"], PEAK_MFMA_16, "TFLOP/s", "mfma")
+    res["roofline"] = _roofline(res["fwdbwd_tflops"], PEAK_MFMA_16, "TFLOP/s", "mfma",
+                                _traffic("c3_fwd", "c3_dkdv", "c3_dq"))
     log(f"[c3] fwd {fwd:.4f} ms ({res['fwd_tflops']:.1f} TF/s), bwd {bwd:.4f} ms "
         f"({res['bwd_tflops']:.1f} TF/s)")
     return res
@@ -196,7 +210,7 @@ def section_c4(steps: int, warmup: int) -> dict:
         "avg_ms": avg, "p50_ms": statistics.median(per), "ms_per_step": avg,
         "kv_gbs": gbs, "kv_gbs_block_granular": block_bytes / (avg * 1e-3) / 1e9,
     }
-    res["roofline"] = _roofline(gbs, PEAK_HBM, "GB/s", "hbm")
+    res["roofline"] = _roofline(gbs, PEAK_HBM, "GB/s", "hbm", _traffic("c4_decode"))
     log(f"[c4] decode step {avg * 1e3:.2f} us, {gbs:.0f} GB/s token-exact "
         f"({100 * gbs / PEAK_HBM:.1f}% of HBM peak)")
     del k, v
@@ -280,6 +294,20 @@ def cpu_baseline(cpu_inputs, kept: int, budget_s: float) -> dict:
                        f"full-step extrapolation {elapsed * H / heads:.1f} s")}
 
 
+def copy_calibration() -> None:
+    """A plain 1 GiB device-to-device copy, three times: the known-size job that
+    FETCH_SIZE / WRITE_SIZE are scaled against (rocprofv3 --pmc)."""
+    import torch
+
+    n = 1 << 29                                   # bf16 elements: 1 GiB
+    a = torch.empty(n, dtype=torch.bfloat16, device="cuda").fill_(1.0)
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    log(f"[copy] copied {a.numel() * 2} bytes x3")
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -288,6 +316,8 @@ def main() -> int:
     ap.add_argument("--sections", default="c2,c3,c4,c5,cpu",
                     help="comma list among c2,c3,c4,c5,cpu (c2 is always run)")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline work")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 1 GiB device copy (counter calibration), print nothing on stdout")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(f"bench.py measures one MI355X only; --gpus {args.gpus} is not supported "
@@ -298,6 +328,9 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a GPU (none visible)", file=sys.stderr)
         return 2
+    if args.copy_calibration:
+        copy_calibration()
+        return 0
     sections = set(s.strip() for s in args.sections.split(","))
     c2, cpu_in = section_c2(args.steps, args.warmup, "cpu" in sections)
     line = {
@@ -319,7 +352,7 @@ def main() -> int:
             "kept_tiles": c2["kept_tiles"], "flops_per_step": c2["flops_per_step"],
             "kernel_avg_ms": round(c2["avg_ms"], 5), "kernel_p50_ms": round(c2["p50_ms"], 5),
         },
-        "roofline": _roofline(c2["tflops"], PEAK_MFMA_16, "TFLOP/s", "mfma"),
+        "roofline": _roofline(c2["tflops"], PEAK_MFMA_16, "TFLOP/s", "mfma", _traffic("c2_fwd")),
     }
     torch.cuda.empty_cache()
     if "c3" in sections:

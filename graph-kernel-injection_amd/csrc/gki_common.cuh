@@ -331,16 +331,39 @@ __device__ inline int xcd_remap(int b, int n) {
   return (xcd < rem) ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
 }
 
+// Reductions across the 4 lane groups (lanes l, l^16, l^32, l^48) with the
+// gfx950 VALU row swaps, no LDS trip. v_permlane32_swap a, b exchanges the
+// upper 32 lanes of a with the lower 32 lanes of b; with a = b = x, lane l then
+// holds {x[l], x[l^32]} in (a, b). v_permlane16_swap does the same for odd /
+// even 16-lane rows ({x[l], x[l^16]}). Inline asm because the compiler's
+// builtin returns the first register for both results (checked on gfx950);
+// the s_nop pairs keep the VALU -> permlane -> VALU wait states.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ inline void swap32(float& a, float& b) {
+  asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+__device__ inline void swap16(float& a, float& b) {
+  asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+#pragma clang diagnostic pop
 __device__ inline float wave_max16x4(float x) {
-  // reduce across the 4 lane groups (lanes l, l^16, l^32, l^48)
-  x = fmaxf(x, __shfl_xor(x, 16));
-  x = fmaxf(x, __shfl_xor(x, 32));
-  return x;
+  float a = x, b = x;
+  swap32(a, b);
+  x = fmaxf(a, b);
+  a = x;
+  b = x;
+  swap16(a, b);
+  return fmaxf(a, b);
 }
 __device__ inline float wave_sum16x4(float x) {
-  x += __shfl_xor(x, 16);
-  x += __shfl_xor(x, 32);
-  return x;
+  float a = x, b = x;
+  swap32(a, b);
+  x = a + b;
+  a = x;
+  b = x;
+  swap16(a, b);
+  return a + b;
 }
 
 constexpr float kLog2e = 1.4426950408889634f;
