@@ -18,8 +18,10 @@ KV GB/s, each as a fraction of the MI355X roofline.
   config 2 (whole heads until ~10 s of CPU time), in the same unit.
 
 Inputs are synthetic N(0, 1) (config 2 scaled by 0.5), generated once and
-resident in HBM before the timed region. Kernel durations come from HIP
-events recorded on the stream the kernels run on (torch's current stream).
+resident in HBM before the timed region. Each section first runs its step
+untimed for --warmup calls and at least WARM_SECONDS of wall time (the GPU's
+clocks ramp up under sustained load), then times. Kernel durations come from
+HIP events recorded on the stream the kernels run on (torch's current stream).
 Prints ONE JSON line on stdout; progress goes to stderr.
 """
 
@@ -54,6 +56,26 @@ def _randn(shape, gen, scale, dtype, device):
     return (torch.randn(shape, generator=gen, dtype=torch.float32) * scale).to(dtype).to(device)
 
 
+# The MI355X ramps its clocks over the first few hundred ms of sustained work:
+# steps timed right after a cold start run up to ~15% slow. Every section keeps
+# calling its step (untimed) until this much wall time has passed.
+WARM_SECONDS = 1.0
+
+
+def _warm(fn, warmup: int) -> None:
+    """``warmup`` untimed calls, then more until WARM_SECONDS have passed."""
+    import torch
+
+    t0 = time.perf_counter()
+    n = 0
+    while n < warmup or time.perf_counter() - t0 < WARM_SECONDS:
+        fn()
+        n += 1
+        if n % 8 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+
+
 def _time_calls(fn, steps: int, warmup: int):
     """Warm up, then time ``steps`` back-to-back calls between one pair of HIP
     events (the throughput a caller's loop sees, launch gaps included), then a
@@ -61,9 +83,7 @@ def _time_calls(fn, steps: int, warmup: int):
     Returns (ms per step from the first pass, per-call ms list)."""
     import torch
 
-    for _ in range(warmup):
-        fn()
-    torch.cuda.synchronize()
+    _warm(fn, warmup)
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0.record()
     for _ in range(steps):
@@ -158,9 +178,7 @@ def section_c3(steps: int, warmup: int) -> dict:
         e[2].record()
         evs.append(e)
 
-    for _ in range(warmup):
-        one()
-    torch.cuda.synchronize()
+    _warm(one, warmup)
     evs.clear()
     t0 = time.perf_counter()
     for _ in range(steps):
@@ -245,9 +263,7 @@ def section_c5(steps: int, warmup: int) -> dict:
         e[2].record()
         evs.append(e)
 
-    for _ in range(warmup):
-        one()
-    torch.cuda.synchronize()
+    _warm(one, warmup)
     evs.clear()
     for _ in range(steps):
         one()
