@@ -102,8 +102,8 @@ __device__ inline void dkdv_tile_of(int b, int BH, int n_kt, int n_heavy, const 
 }
 
 // ---------------------------------------------------------------------------
-// dK / dV, 16-bit. Q and dO tiles row-major in LDS (double-buffered); the
-// dV += P^T dO and dK += dS^T Q operands dO / Q come from lds_tr8.
+// dK / dV, 16-bit. Q and dO tiles row-major in LDS (double-buffered, staged by
+// LDS-DMA); the dV += P^T dO and dK += dS^T Q operands dO / Q come from lds_tr8.
 // ---------------------------------------------------------------------------
 template <typename T, int D>
 __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
@@ -143,29 +143,31 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
   for (int i = 0; i < DT; ++i) dk[i] = dv[i] = floatx4{0.f, 0.f, 0.f, 0.f};
 
   const int e_beg = col_ptr[kt], e_end = col_ptr[kt + 1];
-  Tile tq, tdo;
-  float lreg = 0.f, dreg = 0.f;
-  auto load_tile = [&](int q0) {
-    tq.load(Q + qb, q0, g.n_q, tid);
-    tdo.load(dO + qb, q0, g.n_q, tid);
-    if (tid < 64) {
-      const int r = q0 + tid;
-      lreg = r < g.n_q ? LSE[(size_t)bh * g.n_q + r] * kLog2e : 0.f;
-      dreg = r < g.n_q ? Delta[(size_t)bh * g.n_q + r] : 0.f;
+  DmaTile<D> dma;
+  dma.init(tid);
+  // Q / dO tiles: full tiles by LDS-DMA, the ragged last one through registers
+  // (rows past n_q zero). LSE / Delta rows by a 4-byte LDS-DMA (waves 0 / 1,
+  // one lane per row; rows past n_q re-read row n_q - 1, which only masked
+  // elements see).
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  auto load_tile = [&](int q0, int buf) {
+    if (q0 + kTileM <= g.n_q) {
+      dma.load(Q + qb, q0, sq[buf]);
+      dma.load(dO + qb, q0, sdo[buf]);
+    } else {
+      Tile t;
+      t.load(Q + qb, q0, g.n_q, tid);
+      t.store(sq[buf], tid);
+      t.load(dO + qb, q0, g.n_q, tid);
+      t.store(sdo[buf], tid);
+    }
+    if (wave_u < 2) {
+      const float* src = (wave_u == 0 ? LSE : Delta) + (size_t)bh * g.n_q + min(q0 + lane, g.n_q - 1);
+      dma_load4(src, lds_addr(wave_u == 0 ? slse[buf] : sdlt[buf]));
     }
   };
-  auto store_tile = [&](int buf) {
-    tq.store(sq[buf], tid);
-    tdo.store(sdo[buf], tid);
-    if (tid < 64) {
-      slse[buf][tid] = lreg;
-      sdlt[buf][tid] = dreg;
-    }
-  };
-  if (e_beg < e_end) {
-    load_tile((col_idx[e_beg] & kIdxMask) * kTileM);
-    store_tile(0);
-  }
+  if (e_beg < e_end) load_tile((col_idx[e_beg] & kIdxMask) * kTileM, 0);
+  dma_wait();
   __syncthreads();
 
   const int kv_hi_wave = min(k_w + 15, g.n_kv - 1);
@@ -175,7 +177,7 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
     const int q0 = (ent & kIdxMask) * kTileM;
     const bool partial = (ent >> kPartialBit) & 1;
     const bool has_next = e + 1 < e_end;
-    if (has_next) load_tile((col_idx[e + 1] & kIdxMask) * kTileM);
+    if (has_next) load_tile((col_idx[e + 1] & kIdxMask) * kTileM, buf ^ 1);
     const uint16_t* cq = sq[buf];
     const uint16_t* cdo = sdo[buf];
 
@@ -200,7 +202,7 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
       const int qr0 = rho(t, 4 * grp);
       const float4 lse4 = *(const float4*)(&slse[buf][qr0]);
       const float4 dlt4 = *(const float4*)(&sdlt[buf][qr0]);
-      const float lv[4] = {lse4.x, lse4.y, lse4.z, lse4.w};
+      const float lv[4] = {lse4.x * kLog2e, lse4.y * kLog2e, lse4.z * kLog2e, lse4.w * kLog2e};
       const float dv4[4] = {dlt4.x, dlt4.y, dlt4.z, dlt4.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -220,7 +222,7 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
         dk[dt] = T::mfma(ad, lds_tr8<D>(cq, 32 * st, 16 * dt, lane), dk[dt]);
       }
     }
-    if (has_next) store_tile(buf ^ 1);
+    dma_wait();        // the next tile's LDS-DMA has landed before the barrier
     __syncthreads();
   }
 
@@ -351,7 +353,8 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_32(
 }
 
 // ---------------------------------------------------------------------------
-// dQ, 16-bit. K and V tiles row-major in LDS (double-buffered); the
+// dQ, 16-bit. K and V tiles row-major in LDS (double-buffered, staged by
+// LDS-DMA); the
 // dQ^T += K^T dS^T operand K^T comes from lds_tr8.
 // ---------------------------------------------------------------------------
 template <typename T, int D>
@@ -392,14 +395,24 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_16(
   for (int i = 0; i < DT; ++i) dq[i] = floatx4{0.f, 0.f, 0.f, 0.f};
 
   const int e_beg = row_ptr[qt], e_end = row_ptr[qt + 1];
-  Tile tk, tv;
-  if (e_beg < e_end) {
-    const int k0 = (row_idx[e_beg] & kIdxMask) * kTileN;
-    tk.load(K + kb, k0, g.n_kv, tid);
-    tv.load(V + kb, k0, g.n_kv, tid);
-    tk.store(sk[0], tid);
-    tv.store(sv[0], tid);
-  }
+  DmaTile<D> dma;
+  dma.init(tid);
+  // K / V tiles: full tiles by LDS-DMA, the ragged last one through registers
+  // (rows past n_kv zero).
+  auto stage = [&](int k0, int buf) {
+    if (k0 + kTileN <= g.n_kv) {
+      dma.load(K + kb, k0, sk[buf]);
+      dma.load(V + kb, k0, sv[buf]);
+    } else {
+      Tile t;
+      t.load(K + kb, k0, g.n_kv, tid);
+      t.store(sk[buf], tid);
+      t.load(V + kb, k0, g.n_kv, tid);
+      t.store(sv[buf], tid);
+    }
+  };
+  if (e_beg < e_end) stage((row_idx[e_beg] & kIdxMask) * kTileN, 0);
+  dma_wait();
   __syncthreads();
   const int q_hi_wave = min(q0 + 15, g.n_q - 1);
   for (int e = e_beg; e < e_end; ++e) {
@@ -408,11 +421,7 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_16(
     const int k0 = (ent & kIdxMask) * kTileN;
     const bool partial = (ent >> kPartialBit) & 1;
     const bool has_next = e + 1 < e_end;
-    if (has_next) {
-      const int k1 = (row_idx[e + 1] & kIdxMask) * kTileN;
-      tk.load(K + kb, k1, g.n_kv, tid);
-      tv.load(V + kb, k1, g.n_kv, tid);
-    }
+    if (has_next) stage((row_idx[e + 1] & kIdxMask) * kTileN, buf ^ 1);
     const uint16_t* ck = sk[buf];
     const uint16_t* cv = sv[buf];
     const bool need_mask = partial || (q0 + 15 >= g.n_q) || (k0 + kTileN > g.n_kv) ||
@@ -444,10 +453,7 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_16(
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) dq[dt] = T::mfma(lds_tr8<D>(ck, 32 * st, 16 * dt, lane), b, dq[dt]);
     }
-    if (has_next) {
-      tk.store(sk[buf ^ 1], tid);
-      tv.store(sv[buf ^ 1], tid);
-    }
+    dma_wait();        // the next tile's LDS-DMA has landed before the barrier
     __syncthreads();
   }
   if (my_q < g.n_q) {

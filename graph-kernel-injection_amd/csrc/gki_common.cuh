@@ -204,6 +204,11 @@ __device__ inline void dma_load16(const void* src, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds)
                : "memory", "m0");
 }
+// 4-byte variant: lane i writes lds + 4 i.
+__device__ inline void dma_load4(const void* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(lds)
+               : "memory", "m0");
+}
 #pragma clang diagnostic pop
 // Wait until this wave's vector-memory operations (LDS-DMA included) are done:
 // s_waitcnt vmcnt(0) (gfx9 encoding: vmcnt 0, expcnt 7, lgkmcnt 15). Issued via
