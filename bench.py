@@ -231,8 +231,38 @@ def section_c4(steps: int, warmup: int) -> dict:
     res["roofline"] = _roofline(gbs, PEAK_HBM, "GB/s", "hbm", _traffic("c4_decode"))
     log(f"[c4] decode step {avg * 1e3:.2f} us, {gbs:.0f} GB/s token-exact "
         f"({100 * gbs / PEAK_HBM:.1f}% of HBM peak)")
+    res["rolling_cache"] = _rolling_c4(q, k, v, S, W, fn(), exact_bytes, steps, warmup)
     del k, v
     return res
+
+
+def _rolling_c4(q, k, v, S, W, o_full, exact_bytes, steps, warmup) -> dict:
+    """The same decode from a rolling (sink + ring) cache holding only the
+    positions a query can still see: decode alone, and a full step (append the
+    new token's K/V, then decode)."""
+    import torch
+
+    from gki.kv_cache import StreamingKVCache
+    from sparse_triton_kernel import StreamingMaskSpec
+
+    B, H, NKV, D = k.shape
+    cache = StreamingKVCache(B, H, D, StreamingMaskSpec(S, W), k.dtype, k.device, max_query=1)
+    cache.append(k[:, :, :-1], v[:, :, :-1])
+    o_roll = cache.step(q, k[:, :, -1:], v[:, :, -1:])
+    identical = bool(torch.equal(o_roll, o_full))
+    avg, per = _time_calls(lambda: cache.attend(q), steps, warmup)
+    k1, v1 = k[:, :, -1:].contiguous(), v[:, :, -1:].contiguous()
+    step_avg, _ = _time_calls(lambda: cache.step(q, k1, v1), steps, warmup)
+    gbs = exact_bytes / (avg * 1e-3) / 1e9
+    cache_bytes = 2 * cache.k_cache.numel() * cache.k_cache.element_size()
+    log(f"[c4] rolling cache ({cache.capacity} slots, {cache_bytes / 1e6:.0f} MB vs "
+        f"{2 * k.numel() * k.element_size() / 1e9:.2f} GB full): decode {avg * 1e3:.2f} us "
+        f"({gbs:.0f} GB/s), append+decode step {step_avg * 1e3:.2f} us, "
+        f"bit-identical to the full-cache decode: {identical}")
+    return {"slots": cache.capacity, "cache_bytes": cache_bytes,
+            "full_cache_bytes": 2 * k.numel() * k.element_size(), "decode_ms": avg,
+            "decode_p50_ms": statistics.median(per), "kv_gbs": gbs, "step_ms": step_avg,
+            "identical_to_full_cache": identical}
 
 
 def section_c5(steps: int, warmup: int) -> dict:

@@ -39,6 +39,13 @@ int decode_tokens_dispatch(const Geom& g, const int32_t* list, int n_ent, int32_
 int decode_dispatch(int dtype, int head_dim, const Geom& g, const void* q, const void* k, const void* v,
                     void* o, float* lse, const int32_t* tok, int n_tokens, float* ws, int n_splits,
                     hipStream_t stream);
+void ring_stream(int length, int n_q, int sink, int window, int ring, int* n_sink, int* w_lo, int* base,
+                 int* n_tokens);
+int decode_ring_dispatch(int dtype, int head_dim, const Geom& g, const void* q, const void* k,
+                         const void* v, void* o, float* lse, int ring, float* ws, int n_splits,
+                         hipStream_t stream);
+int append_dispatch(int dtype, int head_dim, void* kc, void* vc, const void* kn, const void* vn, int BH,
+                    int n_new, int start, int sink, int ring, hipStream_t stream);
 
 namespace {
 
@@ -169,6 +176,78 @@ int gki_bsa_decode(const void* q, const void* k, const void* v, void* o, float* 
               "gki_bsa_decode: n_splits must be >= 1 and the grid must fit");
   return decode_dispatch(dtype, head_dim, g, q, k, v, o, lse, tokens, n_tokens, workspace, n_splits,
                          (hipStream_t)stream);
+}
+
+int gki_rolling_stream(int64_t length, int32_t n_q, int32_t sink_size, int32_t window_size,
+                       int32_t ring_size, int32_t* n_sink, int32_t* window_lo, int32_t* n_tokens) {
+  GKI_REQUIRE(n_q >= 1 && n_q <= kDecodeMaxQ, 2, "gki_rolling_stream: n_q must be in [1, 4]");
+  GKI_REQUIRE(length >= n_q && length < (1ll << kPartialBit), 1,
+              "gki_rolling_stream: length must be in [n_q, 2^30)");
+  GKI_REQUIRE(sink_size >= 0 && window_size >= 0, 1,
+              "gki_rolling_stream: sink_size and window_size must be non-negative");
+  GKI_REQUIRE(ring_size >= 1 && (int64_t)ring_size >= (int64_t)window_size + n_q - 1, 1,
+              "gki_rolling_stream: ring_size must be >= window_size + n_q - 1 (and >= 1)");
+  int ns, lo, base, nt;
+  ring_stream((int)length, n_q, sink_size, window_size, ring_size, &ns, &lo, &base, &nt);
+  if (n_sink) *n_sink = ns;
+  if (window_lo) *window_lo = lo;
+  if (n_tokens) *n_tokens = nt;
+  return 0;
+}
+
+int gki_rolling_append(void* k_cache, void* v_cache, const void* k_new, const void* v_new, int32_t dtype,
+                       int32_t B, int32_t H, int32_t head_dim, int32_t sink_size, int32_t ring_size,
+                       int64_t start_pos, int32_t n_new, void* stream) {
+  GKI_REQUIRE(dtype == kF32 || dtype == kF16 || dtype == kBF16, 2,
+              "unsupported dtype code " + std::to_string(dtype) + " (0=fp32, 1=fp16, 2=bf16)");
+  GKI_REQUIRE(head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128, 2,
+              "unsupported head_dim " + std::to_string(head_dim) + " (supported: 16, 32, 64, 128)");
+  GKI_REQUIRE(B > 0 && H > 0 && (int64_t)B * H < (1ll << 31) / 4096, 1,
+              "gki_rolling_append: B and H must be positive and B * H not too large");
+  GKI_REQUIRE(sink_size >= 0 && ring_size >= 1, 1,
+              "gki_rolling_append: sink_size must be >= 0 and ring_size >= 1");
+  GKI_REQUIRE(start_pos >= 0 && n_new >= 0 && start_pos + n_new < (1ll << kPartialBit), 1,
+              "gki_rolling_append: positions must lie in [0, 2^30)");
+  GKI_REQUIRE(n_new == 0 || (k_cache && v_cache && k_new && v_new), 1, "gki_rolling_append: null pointer");
+  if (n_new == 0) return 0;
+  return append_dispatch(dtype, head_dim, k_cache, v_cache, k_new, v_new, B * H, n_new, (int)start_pos,
+                         sink_size, ring_size, (hipStream_t)stream);
+}
+
+int gki_rolling_decode(const void* q, const void* k_cache, const void* v_cache, void* o, float* lse,
+                       int32_t dtype, int32_t B, int32_t H, int32_t n_q, int32_t head_dim,
+                       int32_t sink_size, int32_t window_size, int32_t ring_size, int64_t length,
+                       float softmax_scale, float* workspace, int32_t n_splits, void* stream) {
+  GKI_REQUIRE(dtype == kF32 || dtype == kF16 || dtype == kBF16, 2,
+              "unsupported dtype code " + std::to_string(dtype) + " (0=fp32, 1=fp16, 2=bf16)");
+  GKI_REQUIRE(head_dim == 64 || head_dim == 128, 2,
+              "gki_rolling_decode: head_dim must be 64 or 128, got " + std::to_string(head_dim));
+  GKI_REQUIRE(B > 0 && H > 0 && (int64_t)B * H < (1ll << 31) / 4096, 1,
+              "gki_rolling_decode: B and H must be positive and B * H not too large");
+  if (int rc = gki_rolling_stream(length, n_q, sink_size, window_size, ring_size, nullptr, nullptr,
+                                  nullptr))
+    return rc;
+  GKI_REQUIRE(softmax_scale > 0.f && softmax_scale < __builtin_huge_valf(), 1,
+              "softmax_scale must be positive and finite");
+  GKI_REQUIRE(q && k_cache && v_cache && o && lse, 1, "gki_rolling_decode: null pointer");
+  GKI_REQUIRE(n_splits == 1 || workspace, 1, "gki_rolling_decode: null workspace");
+  GKI_REQUIRE(n_splits >= 1 && (int64_t)n_splits * B * H < (1ll << 31), 1,
+              "gki_rolling_decode: n_splits must be >= 1 and the grid must fit");
+  Geom g{};
+  g.B = B;
+  g.H = H;
+  g.n_q = n_q;
+  g.n_kv = (int)length;                 // positions 0 .. length-1; queries are the last n_q
+  g.q_off = (int)length - n_q;
+  g.scale = softmax_scale;
+  g.scale_log2 = softmax_scale * kLog2e;
+  g.causal = 1;
+  g.sink = sink_size;
+  g.window = window_size;
+  g.mask = nullptr;                     // no stream entry carries the partial flag
+  g.n_qb = g.n_kb = g.bm = g.bn = 1;
+  return decode_ring_dispatch(dtype, head_dim, g, q, k_cache, v_cache, o, lse, ring_size, workspace,
+                              n_splits, (hipStream_t)stream);
 }
 
 }  // extern "C"

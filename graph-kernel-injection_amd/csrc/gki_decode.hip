@@ -95,6 +95,31 @@ __global__ __launch_bounds__(256) void decode_tokens_kernel(Geom g, const int32_
 
 constexpr int kDecodeWaves = 12;   // one 768-thread workgroup per (b, h, split): 3 waves per SIMD
 
+// Token sources of the decode kernel: entry(t) is the t-th entry of the token
+// stream (position | partial << 30), row(e) the K / V row that holds it.
+//   ListTokens: the explicit stream of gki_decode_tokens over a full cache
+//     (row = position).
+//   RingTokens: a rolling cache of `sink` sink slots followed by a ring of
+//     `ring` slots (position p >= sink lives in slot sink + (p - sink) mod ring).
+//     The stream is computed, not loaded: positions 0 .. n_sink-1, then w_lo,
+//     w_lo + 1, ... -- the same ascending positions the full-cache stream holds.
+struct ListTokens {
+  const int32_t* __restrict__ tok;
+  __device__ inline int entry(int t) const { return tok[t]; }
+  __device__ inline int row(int e) const { return e & kIdxMask; }
+};
+
+struct RingTokens {
+  int n_sink, w_lo, sink, ring;
+  int base;                               // (w_lo - sink) mod ring
+  __device__ inline int entry(int t) const { return t < n_sink ? t : w_lo + (t - n_sink); }
+  __device__ inline int row(int e) const {
+    const int p = e & kIdxMask;
+    const int j = base + (p - w_lo);      // in [base, base + ring) for window positions
+    return p < sink ? p : sink + (j >= ring ? j - ring : j);
+  }
+};
+
 // One round of a wave: NU passes of TPW token rows, LPT lanes per row, one
 // 16-byte K and V chunk per lane and pass.
 template <typename T, int D, int NU>
@@ -110,23 +135,24 @@ struct DecodeRound {
   // Rows past the wave's slice read the slice's last entry, flagged by the
   // sign bit: every load stays in range and unconditional (no branch, so no
   // wait is forced on the loads in flight) and the row is masked when consumed.
-  __device__ static inline void positions(const int32_t* __restrict__ tok, int t0, int w1, int tk,
-                                          int (&pos)[NU]) {
+  template <typename Src>
+  __device__ static inline void positions(const Src& src, int t0, int w1, int tk, int (&pos)[NU]) {
 #pragma unroll
     for (int u = 0; u < NU; ++u) {
       const int t = t0 + u * TPW + tk;
-      const int v = tok[t < w1 ? t : w1 - 1];
+      const int v = src.entry(t < w1 ? t : w1 - 1);
       pos[u] = t < w1 ? v : (v | (1 << 31));
     }
   }
-  __device__ inline void fetch(const int (&pos)[NU], int ch, const S* __restrict__ K,
+  template <typename Src>
+  __device__ inline void fetch(const Src& src, const int (&pos)[NU], int ch, const S* __restrict__ K,
                                const S* __restrict__ V, size_t kb) {
 #pragma unroll
     for (int u = 0; u < NU; ++u) pj[u] = pos[u];
 #pragma unroll
-    for (int u = 0; u < NU; ++u) kr[u] = ld_nt16(K + kb + (size_t)(pj[u] & kIdxMask) * D + ch * VEC);
+    for (int u = 0; u < NU; ++u) kr[u] = ld_nt16(K + kb + (size_t)src.row(pj[u]) * D + ch * VEC);
 #pragma unroll
-    for (int u = 0; u < NU; ++u) vr[u] = ld_nt16(V + kb + (size_t)(pj[u] & kIdxMask) * D + ch * VEC);
+    for (int u = 0; u < NU; ++u) vr[u] = ld_nt16(V + kb + (size_t)src.row(pj[u]) * D + ch * VEC);
   }
 };
 
@@ -186,11 +212,13 @@ __device__ inline void decode_consume(const Geom& g, const DecodeRound<T, D, NU>
   }
 }
 
-template <typename T, int D, int NQ>
+// kv_rows: K / V rows per (b, h) (n_kv for a full cache, sink + ring slots for
+// a rolling one).
+template <typename T, int D, int NQ, typename Src>
 __global__ __launch_bounds__(64 * kDecodeWaves) void decode_kernel(
     Geom g, const typename T::storage* __restrict__ Q, const typename T::storage* __restrict__ K,
     const typename T::storage* __restrict__ V, typename T::storage* __restrict__ O,
-    float* __restrict__ LSE, float* __restrict__ ws, const int32_t* __restrict__ tok, int n_tokens,
+    float* __restrict__ LSE, float* __restrict__ ws, Src src, int kv_rows, int n_tokens,
     int n_splits) {
   using S = typename T::storage;
   constexpr int NU = NQ == 1 ? 4 : 2;   // passes per round; two rounds in flight (double-buffered)
@@ -204,7 +232,7 @@ __global__ __launch_bounds__(64 * kDecodeWaves) void decode_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int split = blockIdx.x % n_splits, bh = blockIdx.x / n_splits;
   const size_t qb = (size_t)bh * g.n_q * D;
-  const size_t kb = (size_t)bh * g.n_kv * D;
+  const size_t kb = (size_t)bh * kv_rows * D;
   // this workgroup's slice of the token stream, then this wave's contiguous part
   const int g0 = (int)(((int64_t)n_tokens * split) / n_splits);
   const int g1 = (int)(((int64_t)n_tokens * (split + 1)) / n_splits);
@@ -239,20 +267,20 @@ __global__ __launch_bounds__(64 * kDecodeWaves) void decode_kernel(
   if (w0 < w1) {
     R ra, rb;
     int pa[NU], pb[NU];
-    R::positions(tok, w0, w1, tk, pa);
-    R::positions(tok, w0 + RT, w1, tk, pb);
-    ra.fetch(pa, ch, K, V, kb);
+    R::positions(src, w0, w1, tk, pa);
+    R::positions(src, w0 + RT, w1, tk, pb);
+    ra.fetch(src, pa, ch, K, V, kb);
     for (int t0 = w0; t0 < w1; t0 += 2 * RT) {
       const bool has_b = t0 + RT < w1;
       if (has_b) {
-        R::positions(tok, t0 + 2 * RT, w1, tk, pa);
-        rb.fetch(pb, ch, K, V, kb);
+        R::positions(src, t0 + 2 * RT, w1, tk, pa);
+        rb.fetch(src, pb, ch, K, V, kb);
       }
       decode_consume<T, D, NQ, NU>(g, ra, qv, m, l, acc);
       if (!has_b) break;
       if (t0 + 2 * RT < w1) {
-        R::positions(tok, t0 + 3 * RT, w1, tk, pb);
-        ra.fetch(pa, ch, K, V, kb);
+        R::positions(src, t0 + 3 * RT, w1, tk, pb);
+        ra.fetch(src, pa, ch, K, V, kb);
       }
       decode_consume<T, D, NQ, NU>(g, rb, qv, m, l, acc);
     }
@@ -340,37 +368,103 @@ __global__ __launch_bounds__(64) void combine_kernel(const float* __restrict__ w
   if (lane == 0) LSE[row] = valid ? M * kLn2 + __logf(L) : 0.f;
 }
 
-template <typename T, int D, int NQ>
+template <typename T, int D, int NQ, typename Src>
 int launch_decode_t(const Geom& g, const void* q, const void* k, const void* v, void* o, float* lse,
-                    const int32_t* tok, int n_tokens, float* ws, int n_splits, hipStream_t stream) {
+                    const Src& src, int kv_rows, int n_tokens, float* ws, int n_splits,
+                    hipStream_t stream, const char* what) {
   using S = typename T::storage;
   const int BH = g.B * g.H;
-  hipLaunchKernelGGL((decode_kernel<T, D, NQ>), dim3(BH * n_splits), dim3(64 * kDecodeWaves), 0, stream, g,
-                     (const S*)q, (const S*)k, (const S*)v, (S*)o, lse, ws, tok, n_tokens, n_splits);
+  hipLaunchKernelGGL((decode_kernel<T, D, NQ, Src>), dim3(BH * n_splits), dim3(64 * kDecodeWaves), 0,
+                     stream, g, (const S*)q, (const S*)k, (const S*)v, (S*)o, lse, ws, src, kv_rows,
+                     n_tokens, n_splits);
   if (n_splits > 1)
     hipLaunchKernelGGL((combine_kernel<T, D>), dim3(BH * g.n_q), dim3(64), 0, stream, ws, (S*)o, lse,
                        g.n_q, n_splits);
-  return check_launch("gki_bsa_decode");
+  return check_launch(what);
 }
 
+template <typename Src>
+int launch_decode(int dtype, int head_dim, const Geom& g, const void* q, const void* k, const void* v,
+                  void* o, float* lse, const Src& src, int kv_rows, int n_tokens, float* ws,
+                  int n_splits, hipStream_t stream, const char* what) {
+#define GKI_DECODE_CASE(TT, DD)                                                                   \
+  if (g.n_q == 1)                                                                                 \
+    return launch_decode_t<TT, DD, 1>(g, q, k, v, o, lse, src, kv_rows, n_tokens, ws, n_splits,   \
+                                      stream, what);                                              \
+  return launch_decode_t<TT, DD, kDecodeMaxQ>(g, q, k, v, o, lse, src, kv_rows, n_tokens, ws,     \
+                                              n_splits, stream, what);
+#define GKI_DECODE_DTYPE(TT)                                                                      \
+  if (head_dim == 64) {                                                                           \
+    GKI_DECODE_CASE(TT, 64)                                                                       \
+  }                                                                                               \
+  if (head_dim == 128) {                                                                          \
+    GKI_DECODE_CASE(TT, 128)                                                                      \
+  }                                                                                               \
+  return fail(2, "decode kernel supports head_dim 64 and 128, got " + std::to_string(head_dim));
+  if (dtype == kF32) {
+    GKI_DECODE_DTYPE(F32)
+  }
+  if (dtype == kF16) {
+    GKI_DECODE_DTYPE(F16)
+  }
+  GKI_DECODE_DTYPE(BF16)
+#undef GKI_DECODE_DTYPE
+#undef GKI_DECODE_CASE
+}
+
+// Rolling-cache append: one thread per 16-byte chunk of the rows that survive
+// the call. Of the n_new appended positions start .. end-1, only sink positions
+// (< sink) and the last `ring` positions >= sink are written: earlier ones would
+// be overwritten within the same call, so every slot is written at most once.
+// Rows [0, n_a) of the launch are new rows [0, n_a) (sink part), rows
+// [n_a, n_a + n_b) are new rows [i_b, i_b + n_b) (ring part).
 template <typename T, int D>
-int launch_decode_d(const Geom& g, const void* q, const void* k, const void* v, void* o, float* lse,
-                    const int32_t* tok, int n_tokens, float* ws, int n_splits,
-                    hipStream_t stream) {
-  if (g.n_q == 1)
-    return launch_decode_t<T, D, 1>(g, q, k, v, o, lse, tok, n_tokens, ws, n_splits, stream);
-  return launch_decode_t<T, D, kDecodeMaxQ>(g, q, k, v, o, lse, tok, n_tokens, ws, n_splits, stream);
+__global__ __launch_bounds__(256) void ring_append_kernel(
+    typename T::storage* __restrict__ kc, typename T::storage* __restrict__ vc,
+    const typename T::storage* __restrict__ kn, const typename T::storage* __restrict__ vn, int BH,
+    int n_new, int n_a, int i_b, int n_b, int start, int sink, int ring) {
+  using S = typename T::storage;
+  constexpr int VEC = 16 / sizeof(S);
+  constexpr int CPR = D / VEC;                 // 16-byte chunks per row
+  const int rows = n_a + n_b;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)BH * rows * CPR) return;
+  const int ch = (int)(idx % CPR);
+  const int64_t rr = idx / CPR;
+  const int r = (int)(rr % rows);
+  const int bh = (int)(rr / rows);
+  const int i = r < n_a ? r : i_b + (r - n_a);
+  const int p = start + i;
+  const int slot = p < sink ? p : sink + (p - sink) % ring;
+  const size_t src = ((size_t)bh * n_new + i) * D + ch * VEC;
+  const size_t dst = ((size_t)bh * (sink + ring) + slot) * D + ch * VEC;
+  *(uint4*)(kc + dst) = *(const uint4*)(kn + src);
+  *(uint4*)(vc + dst) = *(const uint4*)(vn + src);
 }
 
 template <typename T>
-int launch_decode(int head_dim, const Geom& g, const void* q, const void* k, const void* v, void* o,
-                  float* lse, const int32_t* tok, int n_tokens, float* ws,
-                  int n_splits, hipStream_t stream) {
-  if (head_dim == 64)
-    return launch_decode_d<T, 64>(g, q, k, v, o, lse, tok, n_tokens, ws, n_splits, stream);
-  if (head_dim == 128)
-    return launch_decode_d<T, 128>(g, q, k, v, o, lse, tok, n_tokens, ws, n_splits, stream);
-  return fail(2, "decode kernel supports head_dim 64 and 128, got " + std::to_string(head_dim));
+int launch_append_t(int head_dim, void* kc, void* vc, const void* kn, const void* vn, int BH, int n_new,
+                    int n_a, int i_b, int n_b, int start, int sink, int ring, hipStream_t stream) {
+  using S = typename T::storage;
+  constexpr int VEC = 16 / sizeof(S);
+  const int64_t total = (int64_t)BH * (n_a + n_b) * (head_dim / VEC);
+  if (total == 0) return 0;
+  const unsigned grid = (unsigned)((total + 255) / 256);
+#define GKI_APPEND_CASE(DD)                                                                       \
+  case DD:                                                                                        \
+    hipLaunchKernelGGL((ring_append_kernel<T, DD>), dim3(grid), dim3(256), 0, stream, (S*)kc,     \
+                       (S*)vc, (const S*)kn, (const S*)vn, BH, n_new, n_a, i_b, n_b, start, sink, \
+                       ring);                                                                     \
+    break;
+  switch (head_dim) {
+    GKI_APPEND_CASE(16)
+    GKI_APPEND_CASE(32)
+    GKI_APPEND_CASE(64)
+    GKI_APPEND_CASE(128)
+    default: return fail(2, "unsupported head_dim " + std::to_string(head_dim));
+  }
+#undef GKI_APPEND_CASE
+  return check_launch("gki_rolling_append");
 }
 
 }  // namespace
@@ -384,13 +478,47 @@ int decode_tokens_dispatch(const Geom& g, const int32_t* list, int n_ent, int32_
 int decode_dispatch(int dtype, int head_dim, const Geom& g, const void* q, const void* k, const void* v,
                     void* o, float* lse, const int32_t* tok, int n_tokens, float* ws,
                     int n_splits, hipStream_t stream) {
-  if (dtype == kF32)
-    return launch_decode<F32>(head_dim, g, q, k, v, o, lse, tok, n_tokens, ws, n_splits, stream);
-  if (dtype == kF16)
-    return launch_decode<F16>(head_dim, g, q, k, v, o, lse, tok, n_tokens, ws, n_splits, stream);
-  return launch_decode<BF16>(head_dim, g, q, k, v, o, lse, tok, n_tokens, ws, n_splits, stream);
+  return launch_decode(dtype, head_dim, g, q, k, v, o, lse, ListTokens{tok}, g.n_kv, n_tokens, ws,
+                       n_splits, stream, "gki_bsa_decode");
 }
 
+// Visible-token stream of the n_q decode rows over a rolling cache of `length`
+// positions: sinks [0, min(sink, length)), then the window positions from
+// w_lo = max(sink, length - n_q - window + 1) to length - 1.
+void ring_stream(int length, int n_q, int sink, int window, int ring, int* n_sink, int* w_lo, int* base,
+                 int* n_tokens) {
+  *n_sink = length < sink ? length : sink;
+  const int lo = length - n_q - window + 1;
+  *w_lo = lo > sink ? lo : sink;
+  *base = (*w_lo - sink) % ring;
+  *n_tokens = *n_sink + (length > *w_lo ? length - *w_lo : 0);
+}
 
+int decode_ring_dispatch(int dtype, int head_dim, const Geom& g, const void* q, const void* k,
+                         const void* v, void* o, float* lse, int ring, float* ws, int n_splits,
+                         hipStream_t stream) {
+  RingTokens src;
+  int n_tokens;
+  ring_stream(g.n_kv, g.n_q, g.sink, g.window, ring, &src.n_sink, &src.w_lo, &src.base, &n_tokens);
+  src.sink = g.sink;
+  src.ring = ring;
+  return launch_decode(dtype, head_dim, g, q, k, v, o, lse, src, g.sink + ring, n_tokens, ws, n_splits,
+                       stream, "gki_rolling_decode");
+}
+
+int append_dispatch(int dtype, int head_dim, void* kc, void* vc, const void* kn, const void* vn, int BH,
+                    int n_new, int start, int sink, int ring, hipStream_t stream) {
+  const int end = start + n_new;
+  const int n_a = start < sink ? (end < sink ? end : sink) - start : 0;
+  const int keep_lo = end - ring > sink ? end - ring : sink;       // first surviving ring position
+  const int b_lo = keep_lo > start ? keep_lo : start;
+  const int i_b = b_lo - start;
+  const int n_b = end > b_lo ? end - b_lo : 0;
+  if (dtype == kF32)
+    return launch_append_t<F32>(head_dim, kc, vc, kn, vn, BH, n_new, n_a, i_b, n_b, start, sink, ring, stream);
+  if (dtype == kF16)
+    return launch_append_t<F16>(head_dim, kc, vc, kn, vn, BH, n_new, n_a, i_b, n_b, start, sink, ring, stream);
+  return launch_append_t<BF16>(head_dim, kc, vc, kn, vn, BH, n_new, n_a, i_b, n_b, start, sink, ring, stream);
+}
 
 }  // namespace gki

@@ -13,6 +13,7 @@ from .fx_pass import (
     _InjectedTritonAttention,
     pretty_print_graph,
 )
+from .kv_cache import StreamingKVCache
 from .lists import BlockLists, build_block_lists, clear_schedule_cache
 from .masks import StreamingMaskSpec, make_dense_mask, make_streaming_mask, streaming_token_mask
 from .ops import _BlockSparseFlashAttention, block_sparse_attention
@@ -24,6 +25,7 @@ __all__ = [
     "InjectionConfig",
     "SingleLayerTransformer",
     "StandardAttention",
+    "StreamingKVCache",
     "StreamingMaskSpec",
     "block_sparse_attention",
     "build_block_lists",

@@ -43,6 +43,10 @@ SIGNATURES = {
                           + [_c_ptr, _c_ptr, _c_ptr]),
     "gki_bsa_decode": (ctypes.c_int, [_c_ptr] * 5 + [_c_int] * 6 + [_c_ptr, _c_int, _c_ptr]
                        + [_c_int] * 4 + [_c_float] + [_c_int] * 3 + [_c_ptr, _c_int, _c_ptr]),
+    "gki_rolling_stream": (ctypes.c_int, [_c_i64] + [_c_int] * 4 + [_c_ptr] * 3),
+    "gki_rolling_append": (ctypes.c_int, [_c_ptr] * 4 + [_c_int] * 6 + [_c_i64, _c_int, _c_ptr]),
+    "gki_rolling_decode": (ctypes.c_int, [_c_ptr] * 5 + [_c_int] * 8 + [_c_i64, _c_float, _c_ptr,
+                                                                       _c_int, _c_ptr]),
 }
 
 _lock = threading.Lock()

@@ -143,6 +143,45 @@ int gki_bsa_decode(const void* q, const void* k, const void* v, void* o, float* 
                    int32_t sink_size, int32_t window_size, float* workspace,
                    int32_t n_splits, void* stream);
 
+/* ---- Rolling StreamingLLM KV cache -------------------------------------------
+ * No reference counterpart: the reference decodes from a full [B, H, N_KV, D]
+ * cache (sparse_triton_kernel.py:636-641) although only S + W tokens are ever
+ * visible (README.md:41-67). A rolling cache holds, per (b, h), `sink_size`
+ * sink slots followed by a ring of `ring_size` slots: position p < sink_size
+ * lives in slot p, position p >= sink_size in slot
+ * sink_size + (p - sink_size) mod ring_size. Cache tensors are
+ * [B, H, sink_size + ring_size, head_dim], contiguous, in the input dtype. For
+ * decode rows n_q the ring must hold window_size + n_q - 1 positions. */
+
+/* Host-only: the visible-token stream of the n_q decode rows (the last n_q of
+ * `length` positions): sinks [0, n_sink), then positions window_lo ..
+ * length - 1; n_tokens = n_sink + max(0, length - window_lo). This is the same
+ * ascending stream gki_decode_tokens yields for a full cache with the
+ * StreamingLLM mask. Any output pointer may be NULL. */
+int gki_rolling_stream(int64_t length, int32_t n_q, int32_t sink_size, int32_t window_size,
+                       int32_t ring_size, int32_t* n_sink, int32_t* window_lo,
+                       int32_t* n_tokens);
+
+/* Append n_new tokens (k_new / v_new: [B, H, n_new, head_dim]) at positions
+ * start_pos .. start_pos + n_new - 1. Positions that a later position of the
+ * same call overwrites are skipped, so each slot is written at most once. */
+int gki_rolling_append(void* k_cache, void* v_cache, const void* k_new, const void* v_new,
+                       int32_t dtype, int32_t B, int32_t H, int32_t head_dim,
+                       int32_t sink_size, int32_t ring_size, int64_t start_pos,
+                       int32_t n_new, void* stream);
+
+/* Decode step over a rolling cache holding positions 0 .. length - 1: the n_q
+ * query rows (q: [B, H, n_q, head_dim]) sit at positions length - n_q ..
+ * length - 1 and see (k <= q) & (k < sink_size | k >= q - window_size + 1).
+ * Same kernel, stream order and split rule as gki_bsa_decode over a full cache
+ * of `length` tokens (bit-identical O and LSE for the same n_splits); the
+ * workspace is sized by gki_bsa_decode_workspace_floats. */
+int gki_rolling_decode(const void* q, const void* k_cache, const void* v_cache, void* o,
+                       float* lse, int32_t dtype, int32_t B, int32_t H, int32_t n_q,
+                       int32_t head_dim, int32_t sink_size, int32_t window_size,
+                       int32_t ring_size, int64_t length, float softmax_scale,
+                       float* workspace, int32_t n_splits, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
