@@ -120,11 +120,13 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
   __shared__ __align__(16) float slse[2][64];
   __shared__ __align__(16) float sdlt[2][64];
 
-  const int BH = g.B * g.H;
+  // one workgroup per (b, kv head, kv tile); with grouped-query attention it
+  // walks the CSC list once per q head of the group, accumulating in registers
+  const int BH = g.B * g.H_kv;
   int bh, kt;
   dkdv_tile_of(blockIdx.x, BH, n_kt, n_heavy, order, bh, kt);
-  const size_t qb = (size_t)bh * g.n_q * D;
   const size_t kb = (size_t)bh * g.n_kv * D;
+  const int bhq0 = (bh / g.H_kv) * g.H + (bh % g.H_kv) * g.group;   // first q head
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int grp = lane >> 4, col = lane & 15;
   const int k_w = kt * kTileN + wave * 16;
@@ -150,7 +152,8 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
   // one lane per row; rows past n_q re-read row n_q - 1, which only masked
   // elements see).
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-  auto load_tile = [&](int q0, int buf) {
+  auto load_tile = [&](int q0, int bhq, int buf) {
+    const size_t qb = (size_t)bhq * g.n_q * D;
     if (q0 + kTileM <= g.n_q) {
       dma.load(Q + qb, q0, sq[buf]);
       dma.load(dO + qb, q0, sdo[buf]);
@@ -162,22 +165,28 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
       t.store(sdo[buf], tid);
     }
     if (wave_u < 2) {
-      const float* src = (wave_u == 0 ? LSE : Delta) + (size_t)bh * g.n_q + min(q0 + lane, g.n_q - 1);
+      const float* src = (wave_u == 0 ? LSE : Delta) + (size_t)bhq * g.n_q + min(q0 + lane, g.n_q - 1);
       dma_load4(src, lds_addr(wave_u == 0 ? slse[buf] : sdlt[buf]));
     }
   };
-  if (e_beg < e_end) load_tile((col_idx[e_beg] & kIdxMask) * kTileM, 0);
+  // iteration i visits list entry e of q head bhq; (e, bhq) advance together
+  const int n_it = (e_end - e_beg) * g.group;
+  int e_nx = e_beg, q_nx = bhq0;
+  if (n_it > 0) load_tile((col_idx[e_beg] & kIdxMask) * kTileM, bhq0, 0);
   dma_wait();
   __syncthreads();
 
   const int kv_hi_wave = min(k_w + 15, g.n_kv - 1);
-  for (int e = e_beg; e < e_end; ++e) {
-    const int buf = (e - e_beg) & 1;
-    const int ent = col_idx[e];
+  for (int it = 0; it < n_it; ++it) {
+    const int buf = it & 1;
+    const int ent = col_idx[e_nx];
+    if (++e_nx == e_end) {
+      e_nx = e_beg;
+      ++q_nx;
+    }
     const int q0 = (ent & kIdxMask) * kTileM;
     const bool partial = (ent >> kPartialBit) & 1;
-    const bool has_next = e + 1 < e_end;
-    if (has_next) load_tile((col_idx[e + 1] & kIdxMask) * kTileM, buf ^ 1);
+    if (it + 1 < n_it) load_tile((col_idx[e_nx] & kIdxMask) * kTileM, q_nx, buf ^ 1);
     const uint16_t* cq = sq[buf];
     const uint16_t* cdo = sdo[buf];
 
@@ -264,11 +273,12 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_32(
   __shared__ __align__(16) DkdvSmem32<D> sm;
   Stage32<D> sq, sdo;
 
-  const int BH = g.B * g.H;
+  // one workgroup per (b, kv head, kv tile), looping over the group's q heads
+  const int BH = g.B * g.H_kv;
   int bh, kt;
   dkdv_tile_of(blockIdx.x, BH, n_kt, n_heavy, order, bh, kt);
-  const size_t qb = (size_t)bh * g.n_q * D;
   const size_t kb = (size_t)bh * g.n_kv * D;
+  const int bhq0 = (bh / g.H_kv) * g.H + (bh % g.H_kv) * g.group;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int grp = lane >> 4, col = lane & 15;
   const int k_w = kt * kTileN + wave * 16;
@@ -287,20 +297,27 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_32(
 
   const int e_beg = col_ptr[kt], e_end = col_ptr[kt + 1];
   float lreg = 0.f, dreg = 0.f;
-  auto load_tile = [&](int q0) {
+  auto load_tile = [&](int q0, int bhq) {
+    const size_t qb = (size_t)bhq * g.n_q * D;
     sq.load(Q + qb, q0, g.n_q, tid);
     sdo.load(dO + qb, q0, g.n_q, tid);
     if (tid < 64) {
       const int r = q0 + tid;
-      lreg = r < g.n_q ? LSE[(size_t)bh * g.n_q + r] * kLog2e : 0.f;
-      dreg = r < g.n_q ? Delta[(size_t)bh * g.n_q + r] : 0.f;
+      lreg = r < g.n_q ? LSE[(size_t)bhq * g.n_q + r] * kLog2e : 0.f;
+      dreg = r < g.n_q ? Delta[(size_t)bhq * g.n_q + r] : 0.f;
     }
   };
-  if (e_beg < e_end) load_tile((col_idx[e_beg] & kIdxMask) * kTileM);
+  const int n_it = (e_end - e_beg) * g.group;
+  int e_nx = e_beg, q_nx = bhq0;
+  if (n_it > 0) load_tile((col_idx[e_beg] & kIdxMask) * kTileM, bhq0);
 
   const int kv_hi_wave = min(k_w + 15, g.n_kv - 1);
-  for (int e = e_beg; e < e_end; ++e) {
-    const int ent = col_idx[e];
+  for (int it = 0; it < n_it; ++it) {
+    const int ent = col_idx[e_nx];
+    if (++e_nx == e_end) {
+      e_nx = e_beg;
+      ++q_nx;
+    }
     const int q0 = (ent & kIdxMask) * kTileM;
     const bool partial = (ent >> kPartialBit) & 1;
     __syncthreads();
@@ -311,7 +328,7 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_32(
       sm.dlt[tid] = dreg;
     }
     __syncthreads();
-    if (e + 1 < e_end) load_tile((col_idx[e + 1] & kIdxMask) * kTileM);
+    if (it + 1 < n_it) load_tile((col_idx[e_nx] & kIdxMask) * kTileM, q_nx);
 
     const bool need_mask = partial || (q0 + kTileM > g.n_q) || (k_w + 15 >= g.n_kv) ||
                            !tile_all_visible(g, q0, min(q0 + kTileM - 1, g.n_q - 1), k_w, kv_hi_wave);
@@ -373,7 +390,7 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_16(
   const int wg = xcd_remap(blockIdx.x, n_wg);
   const int bh = wg / n_qt, qt = wg - bh * n_qt;
   const size_t qb = (size_t)bh * g.n_q * D;
-  const size_t kb = (size_t)bh * g.n_kv * D;
+  const size_t kb = (size_t)kv_bh(g, bh) * g.n_kv * D;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int grp = lane >> 4, col = lane & 15;
   const int q0 = qt * kTileM + wave * 16;
@@ -492,7 +509,7 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_32(
   const int wg = xcd_remap(blockIdx.x, n_wg);
   const int bh = wg / n_qt, qt = wg - bh * n_qt;
   const size_t qb = (size_t)bh * g.n_q * D;
-  const size_t kb = (size_t)bh * g.n_kv * D;
+  const size_t kb = (size_t)kv_bh(g, bh) * g.n_kv * D;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int grp = lane >> 4, col = lane & 15;
   const int q0 = qt * kTileM + wave * 16;
@@ -578,11 +595,11 @@ int launch_bwd(int dtype, const Geom& g, const void* q, const void* k, const voi
                const int32_t* row_ptr, const int32_t* row_idx, int n_qt, const int32_t* col_ptr,
                const int32_t* col_idx, const int32_t* order, int n_heavy, int n_kt,
                hipStream_t stream) {
-  const int BH = g.B * g.H;
+  const int BH = g.B * g.H, BHkv = g.B * g.H_kv;
   const int64_t rows = (int64_t)BH * g.n_q;
   if (dtype == kF32) {
     launch_delta<F32, D>(o, dout, delta, rows, stream);
-    hipLaunchKernelGGL(dkdv_kernel_32<D>, dim3(n_kt * BH), dim3(256), 0, stream, g, (const float*)q,
+    hipLaunchKernelGGL(dkdv_kernel_32<D>, dim3(n_kt * BHkv), dim3(256), 0, stream, g, (const float*)q,
                        (const float*)k, (const float*)v, (const float*)dout, (float*)dk, (float*)dv,
                        lse, delta, col_ptr, col_idx, order, n_heavy, n_kt);
     hipLaunchKernelGGL(dq_kernel_32<D>, dim3(n_qt * BH), dim3(256), 0, stream, g, (const float*)q,
@@ -590,7 +607,7 @@ int launch_bwd(int dtype, const Geom& g, const void* q, const void* k, const voi
                        row_ptr, row_idx, n_qt);
   } else if (dtype == kF16) {
     launch_delta<F16, D>(o, dout, delta, rows, stream);
-    hipLaunchKernelGGL((dkdv_kernel_16<F16, D>), dim3(n_kt * BH), dim3(256), 0, stream, g,
+    hipLaunchKernelGGL((dkdv_kernel_16<F16, D>), dim3(n_kt * BHkv), dim3(256), 0, stream, g,
                        (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
                        (const uint16_t*)dout, (uint16_t*)dk, (uint16_t*)dv, lse, delta, col_ptr,
                        col_idx, order, n_heavy, n_kt);
@@ -599,7 +616,7 @@ int launch_bwd(int dtype, const Geom& g, const void* q, const void* k, const voi
                        (const uint16_t*)dout, (uint16_t*)dq, lse, delta, row_ptr, row_idx, n_qt);
   } else {
     launch_delta<BF16, D>(o, dout, delta, rows, stream);
-    hipLaunchKernelGGL((dkdv_kernel_16<BF16, D>), dim3(n_kt * BH), dim3(256), 0, stream, g,
+    hipLaunchKernelGGL((dkdv_kernel_16<BF16, D>), dim3(n_kt * BHkv), dim3(256), 0, stream, g,
                        (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
                        (const uint16_t*)dout, (uint16_t*)dk, (uint16_t*)dv, lse, delta, col_ptr,
                        col_idx, order, n_heavy, n_kt);

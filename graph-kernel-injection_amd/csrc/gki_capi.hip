@@ -49,14 +49,16 @@ int append_dispatch(int dtype, int head_dim, void* kc, void* vc, const void* kn,
 
 namespace {
 
-int make_geom(Geom& g, int dtype, int B, int H, int n_q, int n_kv, int head_dim, const int32_t* mask,
-              int n_qb, int n_kb, int block_m, int block_n, float scale, int causal, int sink,
-              int window) {
+int make_geom(Geom& g, int dtype, int B, int H, int H_kv, int n_q, int n_kv, int head_dim,
+              const int32_t* mask, int n_qb, int n_kb, int block_m, int block_n, float scale, int causal,
+              int sink, int window) {
   GKI_REQUIRE(dtype == kF32 || dtype == kF16 || dtype == kBF16, 2,
               "unsupported dtype code " + std::to_string(dtype) + " (0=fp32, 1=fp16, 2=bf16)");
   GKI_REQUIRE(head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128, 2,
               "unsupported head_dim " + std::to_string(head_dim) + " (supported: 16, 32, 64, 128)");
   GKI_REQUIRE(B > 0 && H > 0 && n_q > 0 && n_kv > 0, 1, "B, H, n_q and n_kv must be positive");
+  GKI_REQUIRE(H_kv > 0 && H % H_kv == 0, 1,
+              "H_kv must be positive and divide H (grouped-query attention)");
   GKI_REQUIRE((int64_t)B * H < (1ll << 31) / 4096, 1, "B * H too large");
   GKI_REQUIRE(block_m > 0 && block_n > 0, 1, "block_m and block_n must be positive");
   GKI_REQUIRE(n_qb == (n_q + block_m - 1) / block_m && n_kb == (n_kv + block_n - 1) / block_n, 1,
@@ -67,6 +69,8 @@ int make_geom(Geom& g, int dtype, int B, int H, int n_q, int n_kv, int head_dim,
   GKI_REQUIRE(mask != nullptr, 1, "null block mask");
   g.B = B;
   g.H = H;
+  g.H_kv = H_kv;
+  g.group = H / H_kv;
   g.n_q = n_q;
   g.n_kv = n_kv;
   g.q_off = n_kv - n_q;
@@ -90,7 +94,7 @@ using namespace gki;
 
 extern "C" {
 
-int gki_abi_version(void) { return 1; }
+int gki_abi_version(void) { return 2; }
 
 const char* gki_last_error(void) { return g_last_error.c_str(); }
 
@@ -106,12 +110,12 @@ int gki_tile_sizes(int32_t* fwd_tile_m_16, int32_t* fwd_tile_m_32, int32_t* bwd_
 }
 
 int gki_bsa_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int32_t dtype,
-                int32_t B, int32_t H, int32_t n_q, int32_t n_kv, int32_t head_dim,
+                int32_t B, int32_t H, int32_t H_kv, int32_t n_q, int32_t n_kv, int32_t head_dim,
                 const int32_t* row_ptr, const int32_t* row_idx, int32_t n_qt, const int32_t* mask,
                 int32_t n_qb, int32_t n_kb, int32_t block_m, int32_t block_n, float softmax_scale,
                 int32_t is_causal, int32_t sink_size, int32_t window_size, void* stream) {
   Geom g;
-  if (int rc = make_geom(g, dtype, B, H, n_q, n_kv, head_dim, mask, n_qb, n_kb, block_m, block_n,
+  if (int rc = make_geom(g, dtype, B, H, H_kv, n_q, n_kv, head_dim, mask, n_qb, n_kb, block_m, block_n,
                          softmax_scale, is_causal, sink_size, window_size))
     return rc;
   GKI_REQUIRE(q && k && v && o && lse && row_ptr && row_idx, 1, "gki_bsa_fwd: null pointer");
@@ -122,13 +126,13 @@ int gki_bsa_fwd(const void* q, const void* k, const void* v, void* o, float* lse
 
 int gki_bsa_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout,
                 const float* lse, void* dq, void* dk, void* dv, float* delta, int32_t dtype, int32_t B,
-                int32_t H, int32_t n_q, int32_t n_kv, int32_t head_dim, const int32_t* row_ptr,
+                int32_t H, int32_t H_kv, int32_t n_q, int32_t n_kv, int32_t head_dim, const int32_t* row_ptr,
                 const int32_t* row_idx, int32_t n_qt, const int32_t* col_ptr, const int32_t* col_idx,
                 const int32_t* kv_order, int32_t n_heavy, int32_t n_kt, const int32_t* mask,
                 int32_t n_qb, int32_t n_kb, int32_t block_m, int32_t block_n, float softmax_scale,
                 int32_t is_causal, int32_t sink_size, int32_t window_size, void* stream) {
   Geom g;
-  if (int rc = make_geom(g, dtype, B, H, n_q, n_kv, head_dim, mask, n_qb, n_kb, block_m, block_n,
+  if (int rc = make_geom(g, dtype, B, H, H_kv, n_q, n_kv, head_dim, mask, n_qb, n_kb, block_m, block_n,
                          softmax_scale, is_causal, sink_size, window_size))
     return rc;
   GKI_REQUIRE(q && k && v && o && dout && lse && dq && dk && dv && delta, 1, "gki_bsa_bwd: null tensor");
@@ -150,7 +154,7 @@ int gki_decode_tokens(const int32_t* tile_list, int32_t n_tiles, int32_t n_q, in
                       int32_t is_causal, int32_t sink_size, int32_t window_size, int32_t* tokens,
                       int32_t* n_tokens, void* stream) {
   Geom g;
-  if (int rc = make_geom(g, kBF16, 1, 1, n_q, n_kv, 64, mask, n_qb, n_kb, block_m, block_n, 1.f,
+  if (int rc = make_geom(g, kBF16, 1, 1, 1, n_q, n_kv, 64, mask, n_qb, n_kb, block_m, block_n, 1.f,
                          is_causal, sink_size, window_size))
     return rc;
   GKI_REQUIRE(n_tokens && (n_tiles == 0 || (tile_list && tokens)), 1, "gki_decode_tokens: null pointer");
@@ -159,13 +163,13 @@ int gki_decode_tokens(const int32_t* tile_list, int32_t n_tiles, int32_t n_q, in
 }
 
 int gki_bsa_decode(const void* q, const void* k, const void* v, void* o, float* lse, int32_t dtype,
-                   int32_t B, int32_t H, int32_t n_q, int32_t n_kv, int32_t head_dim,
+                   int32_t B, int32_t H, int32_t H_kv, int32_t n_q, int32_t n_kv, int32_t head_dim,
                    const int32_t* tokens, int32_t n_tokens, const int32_t* mask, int32_t n_qb,
                    int32_t n_kb, int32_t block_m, int32_t block_n, float softmax_scale,
                    int32_t is_causal, int32_t sink_size, int32_t window_size, float* workspace,
                    int32_t n_splits, void* stream) {
   Geom g;
-  if (int rc = make_geom(g, dtype, B, H, n_q, n_kv, head_dim, mask, n_qb, n_kb, block_m, block_n,
+  if (int rc = make_geom(g, dtype, B, H, H_kv, n_q, n_kv, head_dim, mask, n_qb, n_kb, block_m, block_n,
                          softmax_scale, is_causal, sink_size, window_size))
     return rc;
   GKI_REQUIRE(q && k && v && o && lse, 1, "gki_bsa_decode: null pointer");
@@ -215,7 +219,7 @@ int gki_rolling_append(void* k_cache, void* v_cache, const void* k_new, const vo
 }
 
 int gki_rolling_decode(const void* q, const void* k_cache, const void* v_cache, void* o, float* lse,
-                       int32_t dtype, int32_t B, int32_t H, int32_t n_q, int32_t head_dim,
+                       int32_t dtype, int32_t B, int32_t H, int32_t H_kv, int32_t n_q, int32_t head_dim,
                        int32_t sink_size, int32_t window_size, int32_t ring_size, int64_t length,
                        float softmax_scale, float* workspace, int32_t n_splits, void* stream) {
   GKI_REQUIRE(dtype == kF32 || dtype == kF16 || dtype == kBF16, 2,
@@ -224,6 +228,8 @@ int gki_rolling_decode(const void* q, const void* k_cache, const void* v_cache, 
               "gki_rolling_decode: head_dim must be 64 or 128, got " + std::to_string(head_dim));
   GKI_REQUIRE(B > 0 && H > 0 && (int64_t)B * H < (1ll << 31) / 4096, 1,
               "gki_rolling_decode: B and H must be positive and B * H not too large");
+  GKI_REQUIRE(H_kv > 0 && H % H_kv == 0, 1,
+              "H_kv must be positive and divide H (grouped-query attention)");
   if (int rc = gki_rolling_stream(length, n_q, sink_size, window_size, ring_size, nullptr, nullptr,
                                   nullptr))
     return rc;
@@ -236,6 +242,8 @@ int gki_rolling_decode(const void* q, const void* k_cache, const void* v_cache, 
   Geom g{};
   g.B = B;
   g.H = H;
+  g.H_kv = H_kv;
+  g.group = H / H_kv;
   g.n_q = n_q;
   g.n_kv = (int)length;                 // positions 0 .. length-1; queries are the last n_q
   g.q_off = (int)length - n_q;

@@ -261,6 +261,14 @@ constexpr int kTileN = 64;       // kv rows of every tile
 constexpr int kTileMF = 128;     // q rows of the forward tile (4 waves x 32 rows)
 constexpr int kDecodeTileM = 16;
 constexpr int kDecodeMaxQ = 4;
+
+// q heads one decode workgroup serves: a whole group of grouped-query heads
+// when its group * n_q rows fit the kernel's row limit (K / V read once per
+// group), else one head.
+inline int decode_heads_per_workgroup(int group, int n_q) {
+  return group > 1 && group * n_q <= kDecodeMaxQ ? group : 1;
+}
+
 constexpr int kPartialBit = 30;       // schedule entry flag: needs per-element mask lookup
 constexpr int kIdxMask = (1 << kPartialBit) - 1;
 
@@ -276,6 +284,7 @@ __device__ inline int rho(int t, int j) {
 // Geometry + masking parameters shared by all attention kernels.
 struct Geom {
   int B, H;
+  int H_kv, group;    // K/V heads and q heads per K/V head (grouped-query attention; 1 = MHA)
   int n_q, n_kv, q_off;
   float scale;        // natural-log softmax scale
   float scale_log2;   // scale * log2(e)
@@ -284,6 +293,11 @@ struct Geom {
   const int32_t* mask;
   int n_qb, n_kb, bm, bn;
 };
+
+// (b, q head) -> (b, kv head) row index of K / V (and dK / dV).
+__device__ inline int kv_bh(const Geom& g, int bh) {
+  return g.group == 1 ? bh : (bh / g.H) * g.H_kv + (bh % g.H) / g.group;
+}
 
 // StreamingLLM token predicate on absolute positions (k <= q) & (k < S | k >= q-W+1).
 __device__ inline bool token_visible(int q_abs, int k, int sink, int window) {

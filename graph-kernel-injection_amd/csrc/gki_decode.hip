@@ -156,8 +156,11 @@ struct DecodeRound {
   }
 };
 
+// Row r of the workgroup is query row qrow[r] (qrow = n_q marks an unused row,
+// which elem_valid rejects).
 template <typename T, int D, int NQ, int NU>
 __device__ inline void decode_consume(const Geom& g, const DecodeRound<T, D, NU>& rd,
+                                      const int (&qrow)[NQ],
                                       const float (&qv)[NQ][16 / sizeof(typename T::storage)],
                                       float (&m)[NQ], float (&l)[NQ],
                                       float (&acc)[NQ][16 / sizeof(typename T::storage)]) {
@@ -178,8 +181,8 @@ __device__ inline void decode_consume(const Geom& g, const DecodeRound<T, D, NU>
       for (int i = 0; i < VEC; ++i) part += qv[r][i] * kf[i];
 #pragma unroll
       for (int off = LPT / 2; off > 0; off >>= 1) part += __shfl_xor(part, off);
-      bool ok = rd.pj[u] >= 0 && r < g.n_q;    // sign bit: padding row of the round
-      if (ok) ok = elem_valid(g, r, rd.pj[u] & kIdxMask, (rd.pj[u] >> kPartialBit) & 1);
+      bool ok = rd.pj[u] >= 0;                 // sign bit: padding row of the round
+      if (ok) ok = elem_valid(g, qrow[r], rd.pj[u] & kIdxMask, (rd.pj[u] >> kPartialBit) & 1);
       sc[r][u] = ok ? part * g.scale_log2 : kNegInf;
     }
   }
@@ -212,14 +215,17 @@ __device__ inline void decode_consume(const Geom& g, const DecodeRound<T, D, NU>
   }
 }
 
-// kv_rows: K / V rows per (b, h) (n_kv for a full cache, sink + ring slots for
-// a rolling one).
+// kv_rows: K / V rows per (b, kv head) (n_kv for a full cache, sink + ring
+// slots for a rolling one). A workgroup serves gq consecutive q heads of one kv
+// head (gq = group when group * n_q <= kDecodeMaxQ, else 1): its n_rows =
+// gq * n_q rows are rows bhq0 * n_q + r of Q / O / LSE, r = head * n_q + query
+// row, and share every K / V load.
 template <typename T, int D, int NQ, typename Src>
 __global__ __launch_bounds__(64 * kDecodeWaves) void decode_kernel(
     Geom g, const typename T::storage* __restrict__ Q, const typename T::storage* __restrict__ K,
     const typename T::storage* __restrict__ V, typename T::storage* __restrict__ O,
     float* __restrict__ LSE, float* __restrict__ ws, Src src, int kv_rows, int n_tokens,
-    int n_splits) {
+    int n_splits, int gq) {
   using S = typename T::storage;
   constexpr int NU = NQ == 1 ? 4 : 2;   // passes per round; two rounds in flight (double-buffered)
   using R = DecodeRound<T, D, NU>;
@@ -230,9 +236,11 @@ __global__ __launch_bounds__(64 * kDecodeWaves) void decode_kernel(
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int split = blockIdx.x % n_splits, bh = blockIdx.x / n_splits;
-  const size_t qb = (size_t)bh * g.n_q * D;
-  const size_t kb = (size_t)bh * kv_rows * D;
+  const int split = blockIdx.x % n_splits, wgh = blockIdx.x / n_splits;
+  const int n_rows = gq * g.n_q;
+  const int bhq0 = wgh * gq;                               // first q head of this workgroup
+  const size_t qb = (size_t)bhq0 * g.n_q * D;
+  const size_t kb = (size_t)kv_bh(g, bhq0) * kv_rows * D;
   // this workgroup's slice of the token stream, then this wave's contiguous part
   const int g0 = (int)(((int64_t)n_tokens * split) / n_splits);
   const int g1 = (int)(((int64_t)n_tokens * (split + 1)) / n_splits);
@@ -241,10 +249,12 @@ __global__ __launch_bounds__(64 * kDecodeWaves) void decode_kernel(
   const int tk = lane / LPT, ch = lane % LPT;
 
   float qv[NQ][VEC];
+  int qrow[NQ];
 #pragma unroll
   for (int r = 0; r < NQ; ++r) {
+    qrow[r] = r < n_rows ? r % g.n_q : g.n_q;
     uint4 raw = make_uint4(0, 0, 0, 0);
-    if (r < g.n_q) raw = *(const uint4*)(Q + qb + (size_t)r * D + ch * VEC);
+    if (r < n_rows) raw = *(const uint4*)(Q + qb + (size_t)r * D + ch * VEC);
     const S* e = (const S*)&raw;
 #pragma unroll
     for (int i = 0; i < VEC; ++i) qv[r][i] = T::to_float(e[i]);
@@ -276,13 +286,13 @@ __global__ __launch_bounds__(64 * kDecodeWaves) void decode_kernel(
         R::positions(src, t0 + 2 * RT, w1, tk, pa);
         rb.fetch(src, pb, ch, K, V, kb);
       }
-      decode_consume<T, D, NQ, NU>(g, ra, qv, m, l, acc);
+      decode_consume<T, D, NQ, NU>(g, ra, qrow, qv, m, l, acc);
       if (!has_b) break;
       if (t0 + 2 * RT < w1) {
         R::positions(src, t0 + 3 * RT, w1, tk, pb);
         ra.fetch(src, pa, ch, K, V, kb);
       }
-      decode_consume<T, D, NQ, NU>(g, rb, qv, m, l, acc);
+      decode_consume<T, D, NQ, NU>(g, rb, qrow, qv, m, l, acc);
     }
   }
   // merge the token-row groups of the wave (same m), then the four waves
@@ -308,8 +318,8 @@ __global__ __launch_bounds__(64 * kDecodeWaves) void decode_kernel(
   }
   __syncthreads();
   const size_t row_stride = D + 2;
-  float* part = ws + ((size_t)bh * n_splits + split) * g.n_q * row_stride;
-  for (int idx = tid; idx < g.n_q * D; idx += 64 * NW) {
+  float* part = ws + ((size_t)wgh * n_splits + split) * n_rows * row_stride;
+  for (int idx = tid; idx < n_rows * D; idx += 64 * NW) {
     const int r = idx / D, d = idx - r * D;
     float M = kNegInf;
 #pragma unroll
@@ -325,7 +335,7 @@ __global__ __launch_bounds__(64 * kDecodeWaves) void decode_kernel(
     if (n_splits == 1) {
       const bool valid = L > 0.f;
       O[qb + (size_t)r * D + d] = T::from_float(valid ? a / L : 0.f);
-      if (d == 0) LSE[(size_t)bh * g.n_q + r] = valid ? M * kLn2 + __logf(L) : 0.f;
+      if (d == 0) LSE[(size_t)bhq0 * g.n_q + r] = valid ? M * kLn2 + __logf(L) : 0.f;
     } else {
       part[r * row_stride + d] = a;
       if (d == 0) {
@@ -370,16 +380,16 @@ __global__ __launch_bounds__(64) void combine_kernel(const float* __restrict__ w
 
 template <typename T, int D, int NQ, typename Src>
 int launch_decode_t(const Geom& g, const void* q, const void* k, const void* v, void* o, float* lse,
-                    const Src& src, int kv_rows, int n_tokens, float* ws, int n_splits,
+                    const Src& src, int kv_rows, int n_tokens, float* ws, int n_splits, int gq,
                     hipStream_t stream, const char* what) {
   using S = typename T::storage;
-  const int BH = g.B * g.H;
-  hipLaunchKernelGGL((decode_kernel<T, D, NQ, Src>), dim3(BH * n_splits), dim3(64 * kDecodeWaves), 0,
+  const int n_wgh = g.B * g.H / gq, n_rows = gq * g.n_q;
+  hipLaunchKernelGGL((decode_kernel<T, D, NQ, Src>), dim3(n_wgh * n_splits), dim3(64 * kDecodeWaves), 0,
                      stream, g, (const S*)q, (const S*)k, (const S*)v, (S*)o, lse, ws, src, kv_rows,
-                     n_tokens, n_splits);
+                     n_tokens, n_splits, gq);
   if (n_splits > 1)
-    hipLaunchKernelGGL((combine_kernel<T, D>), dim3(BH * g.n_q), dim3(64), 0, stream, ws, (S*)o, lse,
-                       g.n_q, n_splits);
+    hipLaunchKernelGGL((combine_kernel<T, D>), dim3(n_wgh * n_rows), dim3(64), 0, stream, ws, (S*)o, lse,
+                       n_rows, n_splits);
   return check_launch(what);
 }
 
@@ -387,12 +397,13 @@ template <typename Src>
 int launch_decode(int dtype, int head_dim, const Geom& g, const void* q, const void* k, const void* v,
                   void* o, float* lse, const Src& src, int kv_rows, int n_tokens, float* ws,
                   int n_splits, hipStream_t stream, const char* what) {
+  const int gq = decode_heads_per_workgroup(g.group, g.n_q);
 #define GKI_DECODE_CASE(TT, DD)                                                                   \
-  if (g.n_q == 1)                                                                                 \
+  if (gq * g.n_q == 1)                                                                            \
     return launch_decode_t<TT, DD, 1>(g, q, k, v, o, lse, src, kv_rows, n_tokens, ws, n_splits,   \
-                                      stream, what);                                              \
+                                      gq, stream, what);                                          \
   return launch_decode_t<TT, DD, kDecodeMaxQ>(g, q, k, v, o, lse, src, kv_rows, n_tokens, ws,     \
-                                              n_splits, stream, what);
+                                              n_splits, gq, stream, what);
 #define GKI_DECODE_DTYPE(TT)                                                                      \
   if (head_dim == 64) {                                                                           \
     GKI_DECODE_CASE(TT, 64)                                                                       \

@@ -48,7 +48,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel_16(
   const int wg = xcd_remap(blockIdx.x, n_wg);
   const int bh = wg / n_qt, qt = wg - bh * n_qt;
   const size_t qb = (size_t)bh * g.n_q * D;
-  const size_t kb = (size_t)bh * g.n_kv * D;
+  const size_t kb = (size_t)kv_bh(g, bh) * g.n_kv * D;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int grp = lane >> 4, col = lane & 15;
   const int qw = qt * kTileMF + wave * 32;   // first row of this wave
@@ -219,7 +219,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel_32(
   const int wg = xcd_remap(blockIdx.x, n_wg);
   const int bh = wg / n_qt, qt = wg - bh * n_qt;
   const size_t qb = (size_t)bh * g.n_q * D;
-  const size_t kb = (size_t)bh * g.n_kv * D;
+  const size_t kb = (size_t)kv_bh(g, bh) * g.n_kv * D;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int grp = lane >> 4, col = lane & 15;
   const int q0 = qt * kTileM + wave * 16;

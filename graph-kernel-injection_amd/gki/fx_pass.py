@@ -98,6 +98,7 @@ class _InjectedTritonAttention(nn.Module):
         is_causal: bool = False,
         sink_size: int = 0,
         window_size: int = 0,
+        enable_gqa: bool = False,
     ) -> None:
         super().__init__()
         self.register_buffer("block_mask", block_mask, persistent=False)
@@ -107,6 +108,9 @@ class _InjectedTritonAttention(nn.Module):
         self.is_causal = bool(is_causal)
         self.sink_size = int(sink_size)
         self.window_size = int(window_size)
+        # grouped-query K/V (fewer heads than Q), as SDPA's enable_gqa; not in the
+        # reference module, whose op requires equal head counts
+        self.enable_gqa = bool(enable_gqa)
 
     def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
         return block_sparse_attention(
@@ -117,6 +121,7 @@ class _InjectedTritonAttention(nn.Module):
             is_causal=self.is_causal,
             sink_size=self.sink_size,
             window_size=self.window_size,
+            enable_gqa=self.enable_gqa,
         )
 
 
@@ -166,6 +171,7 @@ class _SDPAMatch:
     v_node: fx.Node
     is_causal: bool
     scale_value: Optional[float]
+    enable_gqa: bool = False
 
 
 _MATMULS = (torch.matmul, operator.matmul)
@@ -312,7 +318,11 @@ class BlockSparseAttentionInjector:
             scale = _arg(node, "scale", 6, None)
             if scale is not None and not isinstance(scale, (int, float)):
                 continue  # dynamic scale
-            found.append(_SDPAMatch(node, q, k, v, True, None if scale is None else float(scale)))
+            gqa = _arg(node, "enable_gqa", 7, False)
+            if not isinstance(gqa, bool):
+                continue  # dynamic enable_gqa
+            found.append(_SDPAMatch(node, q, k, v, True, None if scale is None else float(scale),
+                                    gqa))
         return found
 
     # -- rewriting -----------------------------------------------------------
@@ -322,12 +332,13 @@ class BlockSparseAttentionInjector:
         return (s.sink_size, s.window_size) if s is not None else (0, default_window)
 
     def _install(self, gm: fx.GraphModule, index: int, anchor: fx.Node, qkv: tuple,
-                 scale: float, is_causal: bool, sink: int, window: int) -> fx.Node:
+                 scale: float, is_causal: bool, sink: int, window: int,
+                 enable_gqa: bool = False) -> fx.Node:
         name = f"_triton_attn_{index}"
         gm.add_submodule(name, _InjectedTritonAttention(
             block_mask=self._mask, softmax_scale=scale,
             block_m=self.cfg.block_m, block_n=self.cfg.block_n,
-            is_causal=is_causal, sink_size=sink, window_size=window,
+            is_causal=is_causal, sink_size=sink, window_size=window, enable_gqa=enable_gqa,
         ))
         with gm.graph.inserting_before(anchor):
             new = gm.graph.call_module(name, args=qkv)
@@ -341,7 +352,7 @@ class BlockSparseAttentionInjector:
         # causal SDPA without StreamingLLM config = plain causal: window spans all keys
         sink, window = self._streaming_params(self.cfg.seq_len_kv)
         self._install(gm, index, match.sdpa_node, (match.q_node, match.k_node, match.v_node),
-                      scale, match.is_causal, sink, window)
+                      scale, match.is_causal, sink, window, match.enable_gqa)
         _safe_erase(gm.graph, match.sdpa_node)
 
     def _install_match(self, gm: fx.GraphModule, match: _AttentionMatch, index: int) -> None:

@@ -58,7 +58,9 @@ def rolling_stream(length: int, n_q: int, sink_size: int, window_size: int,
 class StreamingKVCache:
     """Sink + ring KV cache on the GPU for StreamingLLM decoding.
 
-    ``k_cache`` / ``v_cache``: ``[B, H, sink_size + ring_size, D]`` in ``dtype``.
+    ``k_cache`` / ``v_cache``: ``[B, H, sink_size + ring_size, D]`` in ``dtype``,
+    ``H`` = ``heads`` = the K/V heads. Queries may have any multiple of ``heads``
+    (grouped-query attention: q head h reads kv head h // (Hq // heads)).
     ``length`` counts the positions appended so far (0 .. length-1).
     """
 
@@ -98,9 +100,12 @@ class StreamingKVCache:
     def reset(self) -> None:
         self.length = 0
 
-    def _check_tokens(self, name: str, t: torch.Tensor) -> None:
-        if t.dim() != 4 or tuple(t.shape[:2]) != (self.batch, self.heads) or t.shape[3] != self.head_dim:
-            raise ValueError(f"{name} must be [{self.batch}, {self.heads}, n, {self.head_dim}], "
+    def _check_tokens(self, name: str, t: torch.Tensor, grouped: bool = False) -> None:
+        heads_ok = t.dim() == 4 and (t.shape[1] == self.heads or
+                                     (grouped and t.shape[1] % self.heads == 0 and t.shape[1] > 0))
+        if t.dim() != 4 or t.shape[0] != self.batch or not heads_ok or t.shape[3] != self.head_dim:
+            want = "a multiple of " + str(self.heads) if grouped else str(self.heads)
+            raise ValueError(f"{name} must be [{self.batch}, {want}, n, {self.head_dim}], "
                              f"got {tuple(t.shape)}")
         if t.dtype != self.dtype:
             raise ValueError(f"{name} must be {self.dtype}, got {t.dtype}")
@@ -128,12 +133,13 @@ class StreamingKVCache:
 
     def attend(self, q: torch.Tensor, softmax_scale: Optional[float] = None,
                return_lse: bool = False):
-        """Decode attention of ``q`` (``[B, H, n_q, D]``, the last n_q positions
-        of the cache) over the visible tokens: ``O`` (and the natural-log LSE
-        ``[B, H, n_q]`` fp32 when ``return_lse``)."""
-        from .ops import _decode_splits
+        """Decode attention of ``q`` (``[B, Hq, n_q, D]``, the last n_q positions
+        of the cache; Hq a multiple of the cache's heads) over the visible
+        tokens: ``O`` (and the natural-log LSE ``[B, Hq, n_q]`` fp32 when
+        ``return_lse``)."""
+        from .ops import _decode_slots, _decode_splits
 
-        self._check_tokens("q", q)
+        self._check_tokens("q", q, grouped=True)
         n_q = int(q.shape[2])
         if not 1 <= n_q <= self.max_query:
             raise ValueError(f"q must hold 1..{self.max_query} rows, got {n_q}")
@@ -144,8 +150,9 @@ class StreamingKVCache:
         q = q.contiguous()
         _, _, n_tokens = rolling_stream(self.length, n_q, self.sink_size, self.window_size,
                                         self.ring_size)
-        B, H = self.batch, self.heads
-        n_splits = _decode_splits(n_tokens, B * H)
+        B, H, H_kv = self.batch, int(q.shape[1]), self.heads
+        n_splits = _decode_splits(n_tokens, _decode_slots(B, H, H_kv, n_q,
+                                                          _lib.tile_sizes()["decode_max_q"]))
         o = torch.empty_like(q)
         lse = torch.empty((B, H, n_q), dtype=torch.float32, device=self.device)
         lib = _lib.load()
@@ -159,7 +166,7 @@ class StreamingKVCache:
                 ws_ptr = ws.data_ptr()
             _lib.check(lib.gki_rolling_decode(
                 q.data_ptr(), self.k_cache.data_ptr(), self.v_cache.data_ptr(), o.data_ptr(),
-                lse.data_ptr(), _DTYPE_CODE[self.dtype], B, H, n_q, self.head_dim, self.sink_size,
+                lse.data_ptr(), _DTYPE_CODE[self.dtype], B, H, H_kv, n_q, self.head_dim, self.sink_size,
                 self.window_size, self.ring_size, self.length, float(softmax_scale), ws_ptr,
                 n_splits, stream), "gki_rolling_decode")
         return (o, lse) if return_lse else o

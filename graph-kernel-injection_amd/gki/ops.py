@@ -41,11 +41,20 @@ def _device_mask(block_mask: torch.Tensor, device: torch.device) -> torch.Tensor
 
 
 def _decode_splits(n_tokens: int, bh: int) -> int:
-    """Decode workgroups per (b, h): about one per CU in total, but at least
-    ~1024 tokens (about 85 per wave) per workgroup."""
+    """Decode workgroups per (b, h) slot: about one per CU in total, but at
+    least ~1024 tokens (about 85 per wave) per workgroup."""
     want = -(-_DECODE_TARGET_WGS // bh)
     cap = max(1, n_tokens // 1024)
     return max(1, min(want, cap))
+
+
+def _decode_slots(B: int, H: int, H_kv: int, n_q: int, max_q: int) -> int:
+    """(b, head) slots of the decode grid: a grouped-query group's q heads share
+    one workgroup when group * n_q fits the kernel's rows (the library's
+    ``decode_heads_per_workgroup`` rule), else one q head per workgroup."""
+    group = H // H_kv
+    gq = group if group > 1 and group * n_q <= max_q else 1
+    return B * H // gq
 
 
 class _BlockSparseFlashAttention(torch.autograd.Function):
@@ -64,7 +73,10 @@ class _BlockSparseFlashAttention(torch.autograd.Function):
         is_causal: bool,
         sink_size: int,
         window_size: int,
+        *extra,
     ) -> torch.Tensor:
+        # extra = (enable_gqa,) when given: K / V may have H_kv heads dividing H
+        enable_gqa = bool(extra[0]) if extra else False
         lib = _lib.load()
         if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
             raise ValueError("Q/K/V must be 4-D [B, H, N, D] tensors")
@@ -75,7 +87,9 @@ class _BlockSparseFlashAttention(torch.autograd.Function):
         N_KV = k.shape[2]
         if k.shape != v.shape:
             raise ValueError("K and V must share shape")
-        if k.shape[:2] != q.shape[:2] or k.shape[-1] != D:
+        H_kv = k.shape[1]
+        heads_ok = H_kv == H or (enable_gqa and H_kv > 0 and H % H_kv == 0)
+        if k.shape[0] != B or not heads_ok or k.shape[-1] != D:
             raise ValueError("Q/K/V batch/head/dim mismatch")
         if not (q.dtype == k.dtype == v.dtype) or q.dtype not in _DTYPE_CODE:
             raise ValueError(
@@ -109,7 +123,8 @@ class _BlockSparseFlashAttention(torch.autograd.Function):
             if N_Q <= ts["decode_max_q"] and D in _DECODE_HEAD_DIMS:
                 sched = decode_schedule(block_mask, N_Q, N_KV, block_m, block_n, bool(is_causal),
                                         int(sink_size), int(window_size))
-                n_splits = _decode_splits(sched.n_tokens, B * H)
+                n_splits = _decode_splits(sched.n_tokens,
+                                          _decode_slots(B, H, H_kv, N_Q, ts["decode_max_q"]))
                 ws_ptr = 0
                 if n_splits > 1:
                     ws = torch.empty(int(lib.gki_bsa_decode_workspace_floats(B, H, N_Q, D, n_splits)),
@@ -117,14 +132,14 @@ class _BlockSparseFlashAttention(torch.autograd.Function):
                     ws_ptr = ws.data_ptr()
                 _lib.check(lib.gki_bsa_decode(
                     q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), dtype,
-                    B, H, N_Q, N_KV, D, sched.tokens.data_ptr(), sched.n_tokens, *common,
+                    B, H, H_kv, N_Q, N_KV, D, sched.tokens.data_ptr(), sched.n_tokens, *common,
                     ws_ptr, n_splits, stream), "gki_bsa_decode")
             else:
                 sched = fwd_schedule(block_mask, N_Q, N_KV, block_m, block_n, bool(is_causal),
                                      int(sink_size), int(window_size), q.dtype == torch.float32)
                 _lib.check(lib.gki_bsa_fwd(
                     q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), dtype,
-                    B, H, N_Q, N_KV, D, sched.lists.row_ptr.data_ptr(),
+                    B, H, H_kv, N_Q, N_KV, D, sched.lists.row_ptr.data_ptr(),
                     sched.lists.row_idx.data_ptr(), sched.n_qt, *common, stream), "gki_bsa_fwd")
 
         ctx.save_for_backward(q, k, v, o, lse, block_mask)
@@ -135,6 +150,7 @@ class _BlockSparseFlashAttention(torch.autograd.Function):
         ctx.sink_size = int(sink_size)
         ctx.window_size = int(window_size)
         ctx.q_offset = int(q_offset)
+        ctx.n_extra = len(extra)
         return o
 
     @staticmethod
@@ -145,7 +161,7 @@ class _BlockSparseFlashAttention(torch.autograd.Function):
         q, k, v, o, lse, block_mask = ctx.saved_tensors
         do = do.to(q.dtype).contiguous()
         B, H, N_Q, D = q.shape
-        N_KV = k.shape[2]
+        H_kv, N_KV = k.shape[1], k.shape[2]
         n_qb = (N_Q + ctx.block_m - 1) // ctx.block_m
         n_kb = (N_KV + ctx.block_n - 1) // ctx.block_n
 
@@ -161,12 +177,12 @@ class _BlockSparseFlashAttention(torch.autograd.Function):
             _lib.check(lib.gki_bsa_bwd(
                 q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(),
                 lse.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), delta.data_ptr(),
-                _DTYPE_CODE[q.dtype], B, H, N_Q, N_KV, D, L.row_ptr.data_ptr(),
+                _DTYPE_CODE[q.dtype], B, H, H_kv, N_Q, N_KV, D, L.row_ptr.data_ptr(),
                 L.row_idx.data_ptr(), sched.n_qt, L.col_ptr.data_ptr(), L.col_idx.data_ptr(),
                 sched.kv_order.data_ptr(), sched.n_heavy, sched.n_kt, block_mask.data_ptr(), n_qb,
                 n_kb, ctx.block_m, ctx.block_n, float(ctx.softmax_scale), int(ctx.is_causal),
                 ctx.sink_size, ctx.window_size, stream), "gki_bsa_bwd")
-        return dq, dk, dv, None, None, None, None, None, None, None
+        return (dq, dk, dv) + (None,) * (7 + ctx.n_extra)
 
 
 def block_sparse_attention(
@@ -180,6 +196,7 @@ def block_sparse_attention(
     is_causal: bool = False,
     sink_size: int = 0,
     window_size: int = 0,
+    enable_gqa: bool = False,
 ) -> torch.Tensor:
     """Differentiable block-sparse FlashAttention (``sparse_triton_kernel.py:787-837``).
 
@@ -190,11 +207,16 @@ def block_sparse_attention(
     ``(k <= q) & (k < sink_size | k >= q - window_size + 1)`` with queries
     bottom-right aligned (``q = N_KV - N_Q + row``). ``softmax_scale`` defaults
     to ``1/sqrt(D)``. Rows that see no key produce zeros (and zero gradients).
+
+    ``enable_gqa`` (as in ``F.scaled_dot_product_attention``; not in the
+    reference, which requires equal head counts): K and V may have ``H_kv``
+    heads dividing Q's ``H``; q head ``h`` attends kv head ``h // (H // H_kv)``,
+    and dK / dV sum over each kv head's q heads.
     """
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(q.shape[-1])
-    return _BlockSparseFlashAttention.apply(
-        q.contiguous(), k.contiguous(), v.contiguous(),
-        block_mask, float(softmax_scale), int(block_m), int(block_n),
-        bool(is_causal), int(sink_size), int(window_size),
-    )
+    args = (q.contiguous(), k.contiguous(), v.contiguous(), block_mask, float(softmax_scale),
+            int(block_m), int(block_n), bool(is_causal), int(sink_size), int(window_size))
+    if enable_gqa:
+        args += (True,)
+    return _BlockSparseFlashAttention.apply(*args)

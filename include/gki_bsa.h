@@ -6,6 +6,13 @@
  *  - Tensors are device pointers to contiguous [B, H, N, D] arrays (BHND,
  *    row-major), as produced by `.contiguous()` in the reference
  *    (sparse_triton_kernel.py:834). LSE / Delta are contiguous fp32 [B, H, N_Q].
+ *  - Grouped-query attention: Q / O / dQ have H heads, K / V / dK / dV have
+ *    H_kv heads, H_kv dividing H; q head h reads kv head h / (H / H_kv).
+ *    H_kv == H is the reference's multi-head case (the reference rejects any
+ *    other head count, sparse_triton_kernel.py:640-641). dK / dV of a kv head
+ *    sum the contributions of its H / H_kv q heads in fp32 before the single
+ *    store (no atomics). The decode kernels serve a group's q heads from one
+ *    K / V stream when (H / H_kv) * n_q <= decode_max_q.
  *  - dtype codes: 0 = fp32, 1 = fp16, 2 = bf16. head_dim in {16, 32, 64, 128}.
  *  - The block mask is an int32 [n_qb, n_kb] device array with
  *    n_qb = ceil(N_Q / block_m), n_kb = ceil(N_KV / block_n), shared across B, H.
@@ -27,7 +34,7 @@
 extern "C" {
 #endif
 
-/* ABI version (currently 1). */
+/* ABI version (currently 2: grouped-query attention, H_kv after H). */
 int gki_abi_version(void);
 
 /* Message of the last failing call on this thread. */
@@ -91,7 +98,7 @@ int gki_heavy_order(const int32_t* col_ptr, int32_t n_cols, int32_t* order,
  * row_ptr/row_idx: CSR over ceil(n_q/fwd_tile_m) q tiles (fwd_tile_m_16 or
  * fwd_tile_m_32 by dtype) of kept kv tiles. */
 int gki_bsa_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
-                int32_t dtype, int32_t B, int32_t H, int32_t n_q, int32_t n_kv,
+                int32_t dtype, int32_t B, int32_t H, int32_t H_kv, int32_t n_q, int32_t n_kv,
                 int32_t head_dim, const int32_t* row_ptr, const int32_t* row_idx,
                 int32_t n_qt, const int32_t* mask, int32_t n_qb, int32_t n_kb,
                 int32_t block_m, int32_t block_n, float softmax_scale, int32_t is_causal,
@@ -104,8 +111,8 @@ int gki_bsa_fwd(const void* q, const void* k, const void* v, void* o, float* lse
  * written (no zero-fill needed). */
 int gki_bsa_bwd(const void* q, const void* k, const void* v, const void* o,
                 const void* dout, const float* lse, void* dq, void* dk, void* dv,
-                float* delta, int32_t dtype, int32_t B, int32_t H, int32_t n_q,
-                int32_t n_kv, int32_t head_dim, const int32_t* row_ptr,
+                float* delta, int32_t dtype, int32_t B, int32_t H, int32_t H_kv,
+                int32_t n_q, int32_t n_kv, int32_t head_dim, const int32_t* row_ptr,
                 const int32_t* row_idx, int32_t n_qt, const int32_t* col_ptr,
                 const int32_t* col_idx, const int32_t* kv_order, int32_t n_heavy,
                 int32_t n_kt, const int32_t* mask, int32_t n_qb, int32_t n_kb,
@@ -136,7 +143,7 @@ int gki_decode_tokens(const int32_t* tile_list, int32_t n_tiles, int32_t n_q, in
  * n_splits == 1 they write O / LSE directly, otherwise they write partials to
  * `workspace` and a second launch merges them. Same outputs as gki_bsa_fwd. */
 int gki_bsa_decode(const void* q, const void* k, const void* v, void* o, float* lse,
-                   int32_t dtype, int32_t B, int32_t H, int32_t n_q, int32_t n_kv,
+                   int32_t dtype, int32_t B, int32_t H, int32_t H_kv, int32_t n_q, int32_t n_kv,
                    int32_t head_dim, const int32_t* tokens, int32_t n_tokens,
                    const int32_t* mask, int32_t n_qb, int32_t n_kb, int32_t block_m,
                    int32_t block_n, float softmax_scale, int32_t is_causal,
@@ -177,7 +184,7 @@ int gki_rolling_append(void* k_cache, void* v_cache, const void* k_new, const vo
  * of `length` tokens (bit-identical O and LSE for the same n_splits); the
  * workspace is sized by gki_bsa_decode_workspace_floats. */
 int gki_rolling_decode(const void* q, const void* k_cache, const void* v_cache, void* o,
-                       float* lse, int32_t dtype, int32_t B, int32_t H, int32_t n_q,
+                       float* lse, int32_t dtype, int32_t B, int32_t H, int32_t H_kv, int32_t n_q,
                        int32_t head_dim, int32_t sink_size, int32_t window_size,
                        int32_t ring_size, int64_t length, float softmax_scale,
                        float* workspace, int32_t n_splits, void* stream);

@@ -20,6 +20,10 @@ How each is pinned (by the tests in ``tests/test_oracle_pins.py``):
 * ``tile_classes``        -- build-only tile classification. Pinned per tile
   against ``effective_mask`` (visited iff some effective element; class 1 iff
   the effective mask equals the token rule there).
+* ``expand_kv_heads`` / ``reduce_kv_grad`` -- build-only grouped-query
+  extension. Pinned against torch's repeat_interleave and its autograd
+  adjoint, and (through ``attention_fwd``) against torch's SDPA with
+  ``enable_gqa=True``, which fixes the head mapping h -> h // group.
 * ``attention_fwd/bwd``   -- sparse_triton_kernel.py:845-902 (eager oracle) with
   the kernel's LSE sentinel (:341-352). Pinned against a pure-Python loop on
   tiny inputs, torch's math SDPA with an explicit mask, torch autograd
@@ -202,6 +206,21 @@ def attention_bwd(q: np.ndarray, k: np.ndarray, v: np.ndarray, do: np.ndarray, e
     dq = scale * (ds @ k)
     dk = scale * (np.swapaxes(ds, -1, -2) @ q)
     return dq, dk, dv
+
+
+def expand_kv_heads(t: np.ndarray, group: int) -> np.ndarray:
+    """Grouped-query attention: [B, H_kv, N, D] -> [B, H_kv * group, N, D], q head
+    h reading kv head h // group (build-only extension; torch SDPA's enable_gqa
+    convention, repeat_interleave over the head axis)."""
+    return np.repeat(np.asarray(t), group, axis=1)
+
+
+def reduce_kv_grad(g: np.ndarray, group: int) -> np.ndarray:
+    """Adjoint of ``expand_kv_heads``: dK / dV of a kv head = sum of its
+    group's per-q-head gradients."""
+    g = np.asarray(g)
+    B, H, N, D = g.shape
+    return g.reshape(B, H // group, group, N, D).sum(axis=2)
 
 
 def attention_loop(q: np.ndarray, k: np.ndarray, v: np.ndarray, eff: np.ndarray,

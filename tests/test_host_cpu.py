@@ -94,7 +94,7 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(lib, name), f"{name} declared in gki_bsa.h but not exported"
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
     assert set(_lib.SIGNATURES) == set(names)
-    assert lib.gki_abi_version() == 1
+    assert lib.gki_abi_version() == 2
 
 
 def test_tile_sizes():
@@ -107,23 +107,23 @@ def test_capi_rejects_bad_arguments_before_launch():
     lib = _lib.load()
     null = ctypes.c_void_p(0)
     # unsupported head_dim: code 2, nothing launched
-    rc = lib.gki_bsa_fwd(1, 1, 1, 1, 1, 2, 1, 1, 64, 64, 48, 1, 1, 1, 1, 1, 1, 64, 64, 0.1, 1, 4, 8,
+    rc = lib.gki_bsa_fwd(1, 1, 1, 1, 1, 2, 1, 1, 1, 64, 64, 48, 1, 1, 1, 1, 1, 1, 64, 64, 0.1, 1, 4, 8,
                          null)
     assert rc == 2 and b"head_dim" in lib.gki_last_error()
     # bad dtype code
-    rc = lib.gki_bsa_fwd(1, 1, 1, 1, 1, 7, 1, 1, 64, 64, 64, 1, 1, 1, 1, 1, 1, 64, 64, 0.1, 1, 4, 8,
+    rc = lib.gki_bsa_fwd(1, 1, 1, 1, 1, 7, 1, 1, 1, 64, 64, 64, 1, 1, 1, 1, 1, 1, 64, 64, 0.1, 1, 4, 8,
                          null)
     assert rc == 2 and b"dtype" in lib.gki_last_error()
     # mask shape mismatch
-    rc = lib.gki_bsa_fwd(1, 1, 1, 1, 1, 0, 1, 1, 64, 64, 64, 1, 1, 1, 1, 2, 1, 64, 64, 0.1, 1, 4, 8,
+    rc = lib.gki_bsa_fwd(1, 1, 1, 1, 1, 0, 1, 1, 1, 64, 64, 64, 1, 1, 1, 1, 2, 1, 64, 64, 0.1, 1, 4, 8,
                          null)
     assert rc == 1 and b"mask shape" in lib.gki_last_error()
     # schedule row count mismatch
-    rc = lib.gki_bsa_fwd(1, 1, 1, 1, 1, 0, 1, 1, 200, 64, 64, 1, 1, 2, 1, 4, 1, 64, 64, 0.1, 1, 4, 8,
+    rc = lib.gki_bsa_fwd(1, 1, 1, 1, 1, 0, 1, 1, 1, 200, 64, 64, 1, 1, 2, 1, 4, 1, 64, 64, 0.1, 1, 4, 8,
                          null)
     assert rc == 1 and b"schedule" in lib.gki_last_error()
     # decode: too many rows
-    rc = lib.gki_bsa_decode(1, 1, 1, 1, 1, 2, 1, 1, 8, 64, 64, 1, 1, 1, 1, 1, 64, 64, 0.1, 1, 4, 8,
+    rc = lib.gki_bsa_decode(1, 1, 1, 1, 1, 2, 1, 1, 1, 8, 64, 64, 1, 1, 1, 1, 1, 64, 64, 0.1, 1, 4, 8,
                             1, 1, null)
     assert rc == 2 and b"decode" in lib.gki_last_error()
     # masks
@@ -132,6 +132,10 @@ def test_capi_rejects_bad_arguments_before_launch():
     assert b"divide" in lib.gki_last_error()
     assert lib.gki_bsa_decode_workspace_floats(2, 3, 1, 128, 5) == 2 * 3 * 5 * 130
     # decode: several splits need a workspace
-    rc = lib.gki_bsa_decode(1, 1, 1, 1, 1, 2, 1, 1, 1, 1000, 64, 1, 300, 1, 1, 16, 1, 64, 0.1, 1, 4,
+    rc = lib.gki_bsa_decode(1, 1, 1, 1, 1, 2, 1, 1, 1, 1, 1000, 64, 1, 300, 1, 1, 16, 1, 64, 0.1, 1, 4,
                             8, 0, 2, null)
     assert rc == 1 and b"workspace" in lib.gki_last_error()
+    # grouped-query attention: H_kv must divide H
+    rc = lib.gki_bsa_fwd(1, 1, 1, 1, 1, 2, 1, 6, 4, 64, 64, 64, 1, 1, 1, 1, 1, 1, 64, 64, 0.1, 1, 4,
+                         8, null)
+    assert rc == 1 and b"H_kv" in lib.gki_last_error()

@@ -89,9 +89,9 @@ def test_rolling_capi_rejects_bad_arguments():
     assert lib.gki_rolling_stream(2, 3, 4, 16, 32, None, None, None) == 1
     # decode head_dim limited to 64 / 128; checked before any launch
     null = ctypes.c_void_p(0)
-    rc = lib.gki_rolling_decode(1, 1, 1, 1, 1, 2, 1, 1, 1, 32, 4, 16, 16, 100, 0.1, null, 1, null)
+    rc = lib.gki_rolling_decode(1, 1, 1, 1, 1, 2, 1, 1, 1, 1, 32, 4, 16, 16, 100, 0.1, null, 1, null)
     assert rc == 2 and b"head_dim" in lib.gki_last_error()
-    rc = lib.gki_rolling_decode(None, 1, 1, 1, 1, 2, 1, 1, 1, 64, 4, 16, 16, 100, 0.1, null, 1, null)
+    rc = lib.gki_rolling_decode(None, 1, 1, 1, 1, 2, 1, 1, 1, 1, 64, 4, 16, 16, 100, 0.1, null, 1, null)
     assert rc == 1 and b"null" in lib.gki_last_error()
     rc = lib.gki_rolling_append(1, 1, 1, 1, 2, 1, 1, 64, 4, 16, -1, 1, null)
     assert rc == 1 and b"positions" in lib.gki_last_error()
