@@ -233,7 +233,36 @@ def section_c4(steps: int, warmup: int) -> dict:
         f"({100 * gbs / PEAK_HBM:.1f}% of HBM peak)")
     res["rolling_cache"] = _rolling_c4(q, k, v, S, W, fn(), exact_bytes, steps, warmup)
     del k, v
+    res["gqa"] = _gqa_c4(B, H, NKV, D, S, W, mask, steps, warmup)
     return res
+
+
+def _gqa_c4(B, H, NKV, D, S, W, mask, steps, warmup) -> dict:
+    """The c4 step with grouped-query K/V (8 kv heads for the 32 q heads): each
+    decode workgroup serves a group's 4 q heads from one K/V stream, so the
+    token-exact K/V bytes are a quarter of c4's."""
+    import torch
+
+    import sparse_triton_kernel as stk
+
+    H_kv = 8
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(5)
+    q = torch.randn(B, H, 1, D, generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn(B, H_kv, NKV, D, generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn(B, H_kv, NKV, D, generator=g, device=dev).to(torch.bfloat16)
+
+    def fn():
+        return stk.block_sparse_attention(q, k, v, mask, block_m=1, block_n=64, is_causal=True,
+                                          sink_size=S, window_size=W, enable_gqa=True)
+
+    avg, per = _time_calls(fn, steps, warmup)
+    kv_bytes = (S + W) * D * 2 * 2 * B * H_kv
+    gbs = kv_bytes / (avg * 1e-3) / 1e9
+    log(f"[c4] GQA H{H}/H_kv{H_kv}: decode step {avg * 1e3:.2f} us, {gbs:.0f} GB/s token-exact "
+        f"({kv_bytes / 1e6:.0f} MB of K/V)")
+    return {"workload": f"c4 with grouped-query K/V: H {H}, H_kv {H_kv}", "kv_bytes_token_exact": kv_bytes,
+            "avg_ms": avg, "p50_ms": statistics.median(per), "kv_gbs": gbs}
 
 
 def _rolling_c4(q, k, v, S, W, o_full, exact_bytes, steps, warmup) -> dict:

@@ -10,7 +10,7 @@
 //     query row can see (the hull of sink prefix / window suffix / in-bounds
 //     rows of each tile): S + W positions per head for n_q = 1;
 //   * decode_kernel: workgroup (bh, split) takes an equal slice of that stream
-//     and each of its 12 waves streams a contiguous 1/12 of the slice in
+//     and each of its 12 waves (8 for several rows) streams a contiguous part of the slice in
 //     rounds of 4 token-row passes (16-byte non-temporal K and V loads, D/8
 //     lanes per row), double-buffered: the next round's loads are issued
 //     before the current one is consumed (scores, wave-local online softmax,
@@ -93,7 +93,10 @@ __global__ __launch_bounds__(256) void decode_tokens_kernel(Geom g, const int32_
   if (threadIdx.x == 0) *count = carry;
 }
 
-constexpr int kDecodeWaves = 12;   // one 768-thread workgroup per (b, h, split): 3 waves per SIMD
+// Waves per decode workgroup: 12 (3 per SIMD, 168 VGPRs each) for one query
+// row; 8 (2 per SIMD, 256 VGPRs) for up to four rows, whose per-row scores,
+// query and accumulators would not fit 168 registers.
+template <int NQ> constexpr int decode_waves() { return NQ == 1 ? 12 : 8; }
 
 // Token sources of the decode kernel: entry(t) is the t-th entry of the token
 // stream (position | partial << 30), row(e) the K / V row that holds it.
@@ -221,7 +224,7 @@ __device__ inline void decode_consume(const Geom& g, const DecodeRound<T, D, NU>
 // gq * n_q rows are rows bhq0 * n_q + r of Q / O / LSE, r = head * n_q + query
 // row, and share every K / V load.
 template <typename T, int D, int NQ, typename Src>
-__global__ __launch_bounds__(64 * kDecodeWaves) void decode_kernel(
+__global__ __launch_bounds__(64 * decode_waves<NQ>()) void decode_kernel(
     Geom g, const typename T::storage* __restrict__ Q, const typename T::storage* __restrict__ K,
     const typename T::storage* __restrict__ V, typename T::storage* __restrict__ O,
     float* __restrict__ LSE, float* __restrict__ ws, Src src, int kv_rows, int n_tokens,
@@ -230,7 +233,7 @@ __global__ __launch_bounds__(64 * kDecodeWaves) void decode_kernel(
   constexpr int NU = NQ == 1 ? 4 : 2;   // passes per round; two rounds in flight (double-buffered)
   using R = DecodeRound<T, D, NU>;
   constexpr int VEC = R::VEC, LPT = R::LPT, RT = R::RT;
-  constexpr int NW = kDecodeWaves;
+  constexpr int NW = decode_waves<NQ>();
   __shared__ float wm[NW][NQ], wl[NW][NQ];
   __shared__ float wacc[NW][NQ][D];
 
@@ -384,7 +387,7 @@ int launch_decode_t(const Geom& g, const void* q, const void* k, const void* v, 
                     hipStream_t stream, const char* what) {
   using S = typename T::storage;
   const int n_wgh = g.B * g.H / gq, n_rows = gq * g.n_q;
-  hipLaunchKernelGGL((decode_kernel<T, D, NQ, Src>), dim3(n_wgh * n_splits), dim3(64 * kDecodeWaves), 0,
+  hipLaunchKernelGGL((decode_kernel<T, D, NQ, Src>), dim3(n_wgh * n_splits), dim3(64 * decode_waves<NQ>()), 0,
                      stream, g, (const S*)q, (const S*)k, (const S*)v, (S*)o, lse, ws, src, kv_rows,
                      n_tokens, n_splits, gq);
   if (n_splits > 1)

@@ -15,9 +15,10 @@ mask is turned once, on the GPU, into int32 lists:
   "heavy columns first" order for the dK/dV grid; the decode schedule adds the
   token-exact stream of visible positions.
 
-Schedules are cached per mask tensor (identity, version, geometry); the cache
-holds a reference to the mask so its storage cannot be recycled under the key.
-Building a schedule synchronises the stream once (to size the lists).
+Schedules are cached per mask tensor (identity, version, geometry) and shared
+between tensors of equal content (one build per model, not per layer); the
+cache holds a reference to each mask so its storage cannot be recycled under
+the key. Building a schedule synchronises the stream once (to size the lists).
 """
 
 from __future__ import annotations
@@ -125,21 +126,43 @@ def tile_matrix(mask: torch.Tensor, n_q: int, n_kv: int, block_m: int, block_n: 
 
 
 class _ScheduleCache:
+    """Schedules per mask tensor, shared across tensors of equal content.
+
+    Lookup is by identity first (data pointer, version counter, shape, device).
+    On a miss the mask is compared (``torch.equal``, exact) with the cached
+    masks of the same shape, dtype, device and schedule key that have not been
+    modified in place since their schedule was built; a match reuses that
+    schedule. So the per-layer device copies of one injected mask (the FX pass
+    gives every ``_triton_attn_i`` its own buffer, which ``.to(device)`` copies
+    separately, fx_compiler_pass.py:346-368, 566, 592) share one schedule: one
+    list build per model instead of one per layer.
+    """
+
     def __init__(self, capacity: int = 32) -> None:
-        self._d: "OrderedDict[tuple, Tuple[torch.Tensor, object]]" = OrderedDict()
+        self._d: "OrderedDict[tuple, Tuple[torch.Tensor, int, object]]" = OrderedDict()
         self._cap = capacity
         self._lock = threading.Lock()
 
     def get(self, mask: torch.Tensor, key: tuple, build):
         full = (mask.data_ptr(), mask._version, tuple(mask.shape), mask.device) + key
+        content = (tuple(mask.shape), mask.dtype, mask.device) + key
         with self._lock:
             hit = self._d.get(full)
             if hit is not None and hit[0] is mask:
                 self._d.move_to_end(full)
-                return hit[1]
-        value = build()
+                return hit[2]
+            peers = [(m, ver, val) for k, (m, ver, val) in self._d.items()
+                     if k[2:] == full[2:] and m is not mask and m._version == ver
+                     and (tuple(m.shape), m.dtype, m.device) + key == content]
+        value = None
+        for m, _, val in peers:
+            if torch.equal(m, mask):
+                value = val
+                break
+        if value is None:
+            value = build()
         with self._lock:
-            self._d[full] = (mask, value)
+            self._d[full] = (mask, mask._version, value)
             self._d.move_to_end(full)
             while len(self._d) > self._cap:
                 self._d.popitem(last=False)

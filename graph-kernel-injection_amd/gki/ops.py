@@ -41,10 +41,10 @@ def _device_mask(block_mask: torch.Tensor, device: torch.device) -> torch.Tensor
 
 
 def _decode_splits(n_tokens: int, bh: int) -> int:
-    """Decode workgroups per (b, h) slot: about one per CU in total, but at
-    least ~1024 tokens (about 85 per wave) per workgroup."""
+    """Decode workgroups per (b, head) slot: about one per CU in total, but at
+    least ~256 tokens (a few rounds per wave) per workgroup."""
     want = -(-_DECODE_TARGET_WGS // bh)
-    cap = max(1, n_tokens // 1024)
+    cap = max(1, n_tokens // 256)
     return max(1, min(want, cap))
 
 
