@@ -49,6 +49,11 @@ int append_dispatch(int dtype, int head_dim, void* kc, void* vc, const void* kn,
 
 namespace {
 
+// The kernels move Q / K / V / O (and gradients, K/V caches) in 16-byte chunks
+// (vector loads and LDS-DMA); every such tensor must start 16-byte aligned.
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+template <typename... P> inline bool all_aligned16(P... p) { return (aligned16(p) && ...); }
+
 int make_geom(Geom& g, int dtype, int B, int H, int H_kv, int n_q, int n_kv, int head_dim,
               const int32_t* mask, int n_qb, int n_kb, int block_m, int block_n, float scale, int causal,
               int sink, int window) {
@@ -119,6 +124,7 @@ int gki_bsa_fwd(const void* q, const void* k, const void* v, void* o, float* lse
                          softmax_scale, is_causal, sink_size, window_size))
     return rc;
   GKI_REQUIRE(q && k && v && o && lse && row_ptr && row_idx, 1, "gki_bsa_fwd: null pointer");
+  GKI_REQUIRE(all_aligned16(q, k, v, o), 1, "gki_bsa_fwd: q, k, v, o must be 16-byte aligned");
   const int tm = fwd_tile_m(dtype);
   GKI_REQUIRE(n_qt == (n_q + tm - 1) / tm, 1, "gki_bsa_fwd: schedule row count mismatch");
   return fwd_dispatch(dtype, head_dim, g, q, k, v, o, lse, row_ptr, row_idx, n_qt, (hipStream_t)stream);
@@ -136,6 +142,8 @@ int gki_bsa_bwd(const void* q, const void* k, const void* v, const void* o, cons
                          softmax_scale, is_causal, sink_size, window_size))
     return rc;
   GKI_REQUIRE(q && k && v && o && dout && lse && dq && dk && dv && delta, 1, "gki_bsa_bwd: null tensor");
+  GKI_REQUIRE(all_aligned16(q, k, v, o, dout, dq, dk, dv), 1,
+              "gki_bsa_bwd: q, k, v, o, dout, dq, dk, dv must be 16-byte aligned");
   GKI_REQUIRE(row_ptr && row_idx && col_ptr && col_idx && kv_order, 1, "gki_bsa_bwd: null schedule");
   GKI_REQUIRE(n_qt == (n_q + kTileM - 1) / kTileM && n_kt == (n_kv + kTileN - 1) / kTileN, 1,
               "gki_bsa_bwd: schedule shape mismatch");
@@ -173,6 +181,7 @@ int gki_bsa_decode(const void* q, const void* k, const void* v, void* o, float* 
                          softmax_scale, is_causal, sink_size, window_size))
     return rc;
   GKI_REQUIRE(q && k && v && o && lse, 1, "gki_bsa_decode: null pointer");
+  GKI_REQUIRE(all_aligned16(q, k, v), 1, "gki_bsa_decode: q, k, v must be 16-byte aligned");
   GKI_REQUIRE(n_splits == 1 || workspace, 1, "gki_bsa_decode: null workspace");
   GKI_REQUIRE(n_q <= kDecodeMaxQ, 2, "gki_bsa_decode: n_q exceeds the decode kernel's row limit");
   GKI_REQUIRE(n_tokens >= 0 && (n_tokens == 0 || tokens), 1, "gki_bsa_decode: bad token list");
@@ -213,6 +222,8 @@ int gki_rolling_append(void* k_cache, void* v_cache, const void* k_new, const vo
   GKI_REQUIRE(start_pos >= 0 && n_new >= 0 && start_pos + n_new < (1ll << kPartialBit), 1,
               "gki_rolling_append: positions must lie in [0, 2^30)");
   GKI_REQUIRE(n_new == 0 || (k_cache && v_cache && k_new && v_new), 1, "gki_rolling_append: null pointer");
+  GKI_REQUIRE(n_new == 0 || all_aligned16(k_cache, v_cache, k_new, v_new), 1,
+              "gki_rolling_append: caches and new rows must be 16-byte aligned");
   if (n_new == 0) return 0;
   return append_dispatch(dtype, head_dim, k_cache, v_cache, k_new, v_new, B * H, n_new, (int)start_pos,
                          sink_size, ring_size, (hipStream_t)stream);
@@ -236,6 +247,7 @@ int gki_rolling_decode(const void* q, const void* k_cache, const void* v_cache, 
   GKI_REQUIRE(softmax_scale > 0.f && softmax_scale < __builtin_huge_valf(), 1,
               "softmax_scale must be positive and finite");
   GKI_REQUIRE(q && k_cache && v_cache && o && lse, 1, "gki_rolling_decode: null pointer");
+  GKI_REQUIRE(all_aligned16(q, k_cache, v_cache), 1, "gki_rolling_decode: q and caches must be 16-byte aligned");
   GKI_REQUIRE(n_splits == 1 || workspace, 1, "gki_rolling_decode: null workspace");
   GKI_REQUIRE(n_splits >= 1 && (int64_t)n_splits * B * H < (1ll << 31), 1,
               "gki_rolling_decode: n_splits must be >= 1 and the grid must fit");

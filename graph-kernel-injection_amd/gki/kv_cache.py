@@ -31,6 +31,7 @@ import torch
 
 from . import _lib
 from .masks import StreamingMaskSpec
+from .ops import _aligned, _decode_slots, _decode_splits
 
 _DTYPE_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 _DECODE_HEAD_DIMS = (64, 128)
@@ -121,7 +122,7 @@ class StreamingKVCache:
         n = int(k.shape[2])
         if n == 0:
             return
-        k, v = k.contiguous(), v.contiguous()
+        k, v = _aligned(k), _aligned(v)
         lib = _lib.load()
         with torch.cuda.device(self.device):
             stream = torch.cuda.current_stream(self.device).cuda_stream
@@ -137,8 +138,6 @@ class StreamingKVCache:
         of the cache; Hq a multiple of the cache's heads) over the visible
         tokens: ``O`` (and the natural-log LSE ``[B, Hq, n_q]`` fp32 when
         ``return_lse``)."""
-        from .ops import _decode_slots, _decode_splits
-
         self._check_tokens("q", q, grouped=True)
         n_q = int(q.shape[2])
         if not 1 <= n_q <= self.max_query:
@@ -147,7 +146,7 @@ class StreamingKVCache:
             raise ValueError(f"q has {n_q} rows but the cache holds {self.length} positions")
         if softmax_scale is None:
             softmax_scale = 1.0 / math.sqrt(self.head_dim)
-        q = q.contiguous()
+        q = _aligned(q)
         _, _, n_tokens = rolling_stream(self.length, n_q, self.sink_size, self.window_size,
                                         self.ring_size)
         B, H, H_kv = self.batch, int(q.shape[1]), self.heads

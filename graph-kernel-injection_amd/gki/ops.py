@@ -30,6 +30,14 @@ _DECODE_HEAD_DIMS = (64, 128)
 _DECODE_TARGET_WGS = 256
 
 
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    """Contiguous ``t`` starting on a 16-byte boundary (the kernels move Q / K /
+    V / O in 16-byte chunks; a contiguous view at an odd storage offset is
+    copied)."""
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
 def _device_mask(block_mask: torch.Tensor, device: torch.device) -> torch.Tensor:
     """int32 contiguous copy of the mask on ``device`` (cached for CPU masks)."""
     if block_mask.device == device and block_mask.dtype == torch.int32 and block_mask.is_contiguous():
@@ -106,7 +114,7 @@ class _BlockSparseFlashAttention(torch.autograd.Function):
                 f"block_mask has shape {tuple(block_mask.shape)}, "
                 f"expected {(n_qb, n_kb)}"
             )
-        q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+        q, k, v = _aligned(q), _aligned(k), _aligned(v)
         dev = q.device
         block_mask = _device_mask(block_mask, dev)
 
@@ -159,7 +167,7 @@ class _BlockSparseFlashAttention(torch.autograd.Function):
     ) -> Tuple[Optional[torch.Tensor], ...]:
         lib = _lib.load()
         q, k, v, o, lse, block_mask = ctx.saved_tensors
-        do = do.to(q.dtype).contiguous()
+        do = _aligned(do.to(q.dtype))
         B, H, N_Q, D = q.shape
         H_kv, N_KV = k.shape[1], k.shape[2]
         n_qb = (N_Q + ctx.block_m - 1) // ctx.block_m

@@ -189,6 +189,9 @@ SMALL = [
     (1, 2, 128, 128, 64, 64, 64, 0, 64),
     (1, 2, 128, 128, 64, 64, 64, 4, 0),
     (1, 2, 64, 64, 64, 16, 16, 64, 0),
+    # more queries than keys: q_offset = n_kv - n_q < 0, the first rows see nothing
+    (1, 2, 300, 200, 64, 64, 64, 4, 64),
+    (2, 1, 200, 64, 128, 32, 64, 2, 16),
 ]
 
 
@@ -202,7 +205,8 @@ def test_small_causal_vs_oracle(case, dtype):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("n_q,n_kv,D,bm,bn", [(1, 700, 64, 1, 64), (1, 1000, 128, 1, 64),
                                                (3, 500, 128, 1, 64), (4, 129, 64, 2, 32),
-                                               (1, 64, 128, 1, 64), (2, 2000, 64, 1, 16)])
+                                               (1, 64, 128, 1, 64), (2, 2000, 64, 1, 16),
+                                               (4, 3, 64, 1, 64)])
 def test_decode_vs_oracle(n_q, n_kv, D, bm, bn, dtype):
     _run_case(2, 3, n_q, n_kv, D, dtype, bm, bn, True, 4, 256, seed=n_kv + D, backward=dtype == torch.float32)
 
@@ -350,4 +354,24 @@ def test_fwd_bwd_deterministic():
         out.backward(do)
         runs.append([out.detach()] + [t.grad for t in leaves])
     for a, b in zip(*runs):
+        assert torch.equal(a, b)
+
+
+def test_misaligned_views_are_copied_not_faulted():
+    """Contiguous views at an odd storage offset (2 bytes off a 16-byte
+    boundary) give exactly the aligned result, forward and backward."""
+    B, H, N, D = 1, 2, 300, 64
+    n = B * H * N * D
+    g = torch.Generator().manual_seed(21)
+    base = [torch.randn(n + 8, generator=g).to(torch.bfloat16).to(DEV) for _ in range(4)]
+    q, k, v, do = (b[1:1 + n].view(B, H, N, D) for b in base)
+    assert q.is_contiguous() and q.data_ptr() % 16 != 0
+    mask = stk.make_streaming_mask(N, N, stk.StreamingMaskSpec(4, 64), 64, 64, device=DEV)
+    outs = []
+    for qq, kk, vv in ((q, k, v), (q.clone(), k.clone(), v.clone())):
+        leaves = [t.detach().requires_grad_(True) for t in (qq, kk, vv)]
+        o = stk.block_sparse_attention(*leaves, mask, is_causal=True, sink_size=4, window_size=64)
+        o.backward(do)
+        outs.append([o] + [t.grad for t in leaves])
+    for a, b in zip(*outs):
         assert torch.equal(a, b)

@@ -119,12 +119,12 @@ def test_capi_rejects_bad_arguments_before_launch():
                          null)
     assert rc == 1 and b"mask shape" in lib.gki_last_error()
     # schedule row count mismatch
-    rc = lib.gki_bsa_fwd(1, 1, 1, 1, 1, 0, 1, 1, 1, 200, 64, 64, 1, 1, 2, 1, 4, 1, 64, 64, 0.1, 1, 4, 8,
-                         null)
+    rc = lib.gki_bsa_fwd(16, 16, 16, 16, 16, 0, 1, 1, 1, 200, 64, 64, 16, 16, 2, 1, 4, 1, 64, 64,
+                         0.1, 1, 4, 8, null)
     assert rc == 1 and b"schedule" in lib.gki_last_error()
     # decode: too many rows
-    rc = lib.gki_bsa_decode(1, 1, 1, 1, 1, 2, 1, 1, 1, 8, 64, 64, 1, 1, 1, 1, 1, 64, 64, 0.1, 1, 4, 8,
-                            1, 1, null)
+    rc = lib.gki_bsa_decode(16, 16, 16, 16, 16, 2, 1, 1, 1, 8, 64, 64, 1, 1, 1, 1, 1, 64, 64, 0.1,
+                            1, 4, 8, 1, 1, null)
     assert rc == 2 and b"decode" in lib.gki_last_error()
     # masks
     assert lib.gki_streaming_mask(1, 0, 10, 4, 4, 64, 64, null) == 1
@@ -132,9 +132,13 @@ def test_capi_rejects_bad_arguments_before_launch():
     assert b"divide" in lib.gki_last_error()
     assert lib.gki_bsa_decode_workspace_floats(2, 3, 1, 128, 5) == 2 * 3 * 5 * 130
     # decode: several splits need a workspace
-    rc = lib.gki_bsa_decode(1, 1, 1, 1, 1, 2, 1, 1, 1, 1, 1000, 64, 1, 300, 1, 1, 16, 1, 64, 0.1, 1, 4,
-                            8, 0, 2, null)
+    rc = lib.gki_bsa_decode(16, 16, 16, 16, 16, 2, 1, 1, 1, 1, 1000, 64, 1, 300, 1, 1, 16, 1, 64,
+                            0.1, 1, 4, 8, 0, 2, null)
     assert rc == 1 and b"workspace" in lib.gki_last_error()
+    # misaligned tensor pointers are rejected before any launch
+    rc = lib.gki_bsa_fwd(16, 18, 16, 16, 16, 2, 1, 1, 1, 64, 64, 64, 16, 16, 1, 16, 1, 1, 64, 64,
+                         0.1, 1, 4, 8, null)
+    assert rc == 1 and b"aligned" in lib.gki_last_error()
     # grouped-query attention: H_kv must divide H
     rc = lib.gki_bsa_fwd(1, 1, 1, 1, 1, 2, 1, 6, 4, 64, 64, 64, 1, 1, 1, 1, 1, 1, 64, 64, 0.1, 1, 4,
                          8, null)
