@@ -44,6 +44,11 @@ struct F16 {
   }
   // eight 1.0 elements: an all-ones MFMA operand (row sums on the matrix pipe)
   __device__ static inline uint4 ones8() { return make_uint4(0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u); }
+  // a.lo * b.lo + a.hi * b.hi + c in fp32 on packed pairs (v_dot2_f32_f16)
+  __device__ static inline float dot2(uint32_t a, uint32_t b, float c) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a), __builtin_bit_cast(h2, b), c, false);
+  }
 };
 struct BF16 {
   using storage = uint16_t;
@@ -60,6 +65,11 @@ struct BF16 {
                                                     __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   }
   __device__ static inline uint4 ones8() { return make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u); }
+  // a.lo * b.lo + a.hi * b.hi + c in fp32 on packed pairs (v_dot2_f32_bf16)
+  __device__ static inline float dot2(uint32_t a, uint32_t b, float c) {
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2, a), __builtin_bit_cast(b2, b), c, false);
+  }
 };
 
 __device__ inline floatx4 mfma_f32(float a, float b, floatx4 c) {
@@ -366,6 +376,61 @@ __device__ inline void swap16(float& a, float& b) {
   asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
 }
 #pragma clang diagnostic pop
+// DPP row permute of a float (VALU rate, no LDS): CTRL is a gfx9 dpp_ctrl
+// code; all rows / banks enabled, every source lane lies in the same 16-lane row.
+template <int CTRL>
+__device__ inline float dpp_perm(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL,
+                                                               0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // lane i of each 8 reads lane 7-i
+constexpr int kDppMirror = 0x140;     // lane i of each 16 reads lane 15-i
+
+// Sum over aligned groups of N lanes (N a power of two, 1..64); every lane gets
+// its group's sum. Once the lanes of each quad (8, 16-lane half) hold equal
+// values, the mirrors pair each with the other quad (half): no LDS traffic.
+template <int N>
+__device__ inline float group_sum(float x) {
+  if constexpr (N >= 2) x += dpp_perm<kDppXor1>(x);
+  if constexpr (N >= 4) x += dpp_perm<kDppXor2>(x);
+  if constexpr (N >= 8) x += dpp_perm<kDppHalfMirror>(x);
+  if constexpr (N >= 16) x += dpp_perm<kDppMirror>(x);
+  if constexpr (N >= 32) {
+    float a = x, b = x;
+    swap16(a, b);
+    x = a + b;
+  }
+  if constexpr (N >= 64) {
+    float a = x, b = x;
+    swap32(a, b);
+    x = a + b;
+  }
+  return x;
+}
+
+// Max across the 64/N aligned groups of N lanes, for values that are uniform
+// within each group (so any pairing of whole groups is a valid exchange).
+template <int N>
+__device__ inline float cross_group_max(float x) {
+  if constexpr (N <= 1) x = fmaxf(x, dpp_perm<kDppXor1>(x));
+  if constexpr (N <= 2) x = fmaxf(x, dpp_perm<kDppXor2>(x));
+  if constexpr (N <= 4) x = fmaxf(x, dpp_perm<kDppHalfMirror>(x));
+  if constexpr (N <= 8) x = fmaxf(x, dpp_perm<kDppMirror>(x));
+  if constexpr (N <= 16) {
+    float a = x, b = x;
+    swap16(a, b);
+    x = fmaxf(a, b);
+  }
+  if constexpr (N <= 32) {
+    float a = x, b = x;
+    swap32(a, b);
+    x = fmaxf(a, b);
+  }
+  return x;
+}
+
 __device__ inline float wave_max16x4(float x) {
   float a = x, b = x;
   swap32(a, b);

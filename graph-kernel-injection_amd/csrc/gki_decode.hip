@@ -159,12 +159,37 @@ struct DecodeRound {
   }
 };
 
+// A lane's slice of the workgroup's query rows and its dot product with one
+// 16-byte K chunk: 16-bit inputs stay packed and go through v_dot2_f32_* (the
+// products are exact in fp32, accumulation in fp32); fp32 inputs use FMAs.
+template <typename T, int NQ>
+struct DecodeQ {
+  uint4 raw[NQ];
+  __device__ inline float dot(int r, const uint4& k) const {
+    float p = T::dot2(raw[r].x, k.x, 0.f);
+    p = T::dot2(raw[r].y, k.y, p);
+    p = T::dot2(raw[r].z, k.z, p);
+    return T::dot2(raw[r].w, k.w, p);
+  }
+};
+template <int NQ>
+struct DecodeQ<F32, NQ> {
+  uint4 raw[NQ];
+  __device__ inline float dot(int r, const uint4& k) const {
+    const float* q = (const float*)&raw[r];
+    const float* kf = (const float*)&k;
+    float p = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p += q[i] * kf[i];
+    return p;
+  }
+};
+
 // Row r of the workgroup is query row qrow[r] (qrow = n_q marks an unused row,
 // which elem_valid rejects).
 template <typename T, int D, int NQ, int NU>
 __device__ inline void decode_consume(const Geom& g, const DecodeRound<T, D, NU>& rd,
-                                      const int (&qrow)[NQ],
-                                      const float (&qv)[NQ][16 / sizeof(typename T::storage)],
+                                      const int (&qrow)[NQ], const DecodeQ<T, NQ>& qv,
                                       float (&m)[NQ], float (&l)[NQ],
                                       float (&acc)[NQ][16 / sizeof(typename T::storage)]) {
   using S = typename T::storage;
@@ -173,17 +198,10 @@ __device__ inline void decode_consume(const Geom& g, const DecodeRound<T, D, NU>
   float sc[NQ][NU];
 #pragma unroll
   for (int u = 0; u < NU; ++u) {
-    const S* e = (const S*)&rd.kr[u];
-    float kf[VEC];
-#pragma unroll
-    for (int i = 0; i < VEC; ++i) kf[i] = T::to_float(e[i]);
 #pragma unroll
     for (int r = 0; r < NQ; ++r) {
-      float part = 0.f;
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) part += qv[r][i] * kf[i];
-#pragma unroll
-      for (int off = LPT / 2; off > 0; off >>= 1) part += __shfl_xor(part, off);
+      float part = qv.dot(r, rd.kr[u]);
+      part = group_sum<LPT>(part);             // the LPT lanes of a token row
       bool ok = rd.pj[u] >= 0;                 // sign bit: padding row of the round
       if (ok) ok = elem_valid(g, qrow[r], rd.pj[u] & kIdxMask, (rd.pj[u] >> kPartialBit) & 1);
       sc[r][u] = ok ? part * g.scale_log2 : kNegInf;
@@ -194,8 +212,7 @@ __device__ inline void decode_consume(const Geom& g, const DecodeRound<T, D, NU>
     float mx = kNegInf;
 #pragma unroll
     for (int u = 0; u < NU; ++u) mx = fmaxf(mx, sc[r][u]);
-#pragma unroll
-    for (int off = LPT; off < 64; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    mx = cross_group_max<LPT>(mx);             // scores are uniform within a token row
     const float m_new = fmaxf(m[r], mx);
     const float mu = m_new == kNegInf ? 0.f : m_new;
     const float alpha = __builtin_amdgcn_exp2f(m[r] - mu);
@@ -230,7 +247,7 @@ __global__ __launch_bounds__(64 * decode_waves<NQ>()) void decode_kernel(
     float* __restrict__ LSE, float* __restrict__ ws, Src src, int kv_rows, int n_tokens,
     int n_splits, int gq) {
   using S = typename T::storage;
-  constexpr int NU = NQ == 1 ? 4 : 2;   // passes per round; two rounds in flight (double-buffered)
+  constexpr int NU = NQ == 1 ? 4 : 3;   // passes per round; two rounds in flight (double-buffered)
   using R = DecodeRound<T, D, NU>;
   constexpr int VEC = R::VEC, LPT = R::LPT, RT = R::RT;
   constexpr int NW = decode_waves<NQ>();
@@ -251,16 +268,12 @@ __global__ __launch_bounds__(64 * decode_waves<NQ>()) void decode_kernel(
   const int w1 = g0 + (int)(((int64_t)(g1 - g0) * (wave + 1)) / NW);
   const int tk = lane / LPT, ch = lane % LPT;
 
-  float qv[NQ][VEC];
+  DecodeQ<T, NQ> qv;
   int qrow[NQ];
 #pragma unroll
   for (int r = 0; r < NQ; ++r) {
     qrow[r] = r < n_rows ? r % g.n_q : g.n_q;
-    uint4 raw = make_uint4(0, 0, 0, 0);
-    if (r < n_rows) raw = *(const uint4*)(Q + qb + (size_t)r * D + ch * VEC);
-    const S* e = (const S*)&raw;
-#pragma unroll
-    for (int i = 0; i < VEC; ++i) qv[r][i] = T::to_float(e[i]);
+    qv.raw[r] = r < n_rows ? *(const uint4*)(Q + qb + (size_t)r * D + ch * VEC) : make_uint4(0, 0, 0, 0);
   }
   // wave-local online softmax state; m is uniform across the wave, l and acc
   // are per token-row group and summed at the end
