@@ -431,15 +431,19 @@ __device__ inline float cross_group_max(float x) {
   return x;
 }
 
+// Swaps and maxes in one asm block: through fmaxf the compiler canonicalises
+// both asm outputs (v_max x, x, x) before every max.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 __device__ inline float wave_max16x4(float x) {
   float a = x, b = x;
-  swap32(a, b);
-  x = fmaxf(a, b);
-  a = x;
-  b = x;
-  swap16(a, b);
-  return fmaxf(a, b);
+  asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1\n\tv_max_f32 %0, %0, %1\n\t"
+      "v_mov_b32 %1, %0\n\ts_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1\n\t"
+      "v_max_f32 %0, %0, %1"
+      : "+v"(a), "+v"(b));
+  return a;
 }
+#pragma clang diagnostic pop
 __device__ inline float wave_sum16x4(float x) {
   float a = x, b = x;
   swap32(a, b);
