@@ -6,9 +6,9 @@
 // (n_q <= 4 query rows at the end of the KV cache, q_offset = n_kv - n_q) is a
 // bandwidth-bound split-KV pass:
 //   * decode_tokens_kernel (once per mask, cached by the host) expands the kept
-//     kv tiles of the single decode q tile into the positions of the tokens any
-//     query row can see (the hull of sink prefix / window suffix / in-bounds
-//     rows of each tile): S + W positions per head for n_q = 1;
+//     kv tiles of the single decode q tile into exactly the positions some query
+//     row can see (per tile its sink run and its window run): S + W positions
+//     per head for n_q = 1;
 //   * decode_kernel: workgroup (bh, split) takes an equal slice of that stream
 //     and each of its 12 waves (8 for several rows) streams a contiguous part of the slice in
 //     rounds of 4 token-row passes (16-byte non-temporal K and V loads, D/8
@@ -31,29 +31,35 @@ namespace gki {
 namespace {
 
 
-// Hull [lo, hi) of the tokens of kv tile `kt` visible to any of the n_q rows.
-__device__ inline void tile_hull(const Geom& g, int kt, int& lo, int& hi) {
-  lo = kt * kTileN;
-  hi = min(lo + kTileN, g.n_kv);
+// The tokens of kv tile `kt` that some of the n_q rows can see, as at most two
+// ascending runs [lo1, hi1), [lo2, hi2): the sink run and the window run (one
+// run when they touch; the whole in-bounds tile when not causal). The stream is
+// exactly the union of the rows' visible positions, so for a single query row
+// no token in it needs the token rule.
+__device__ inline void tile_runs(const Geom& g, int kt, int& lo1, int& hi1, int& lo2, int& hi2) {
+  const int lo = kt * kTileN, hi = min(lo + kTileN, g.n_kv);
+  lo1 = lo;
+  hi1 = hi;
+  lo2 = hi2 = 0;
   if (!g.causal || lo >= hi) return;
   const int qa = g.q_off, qb = g.n_kv - 1;          // absolute positions of rows 0 and n_q-1
   const int a_hi = min(hi, qb + 1);
-  int h_lo = 0x7fffffff, h_hi = -1;
-  const int s_hi = min(a_hi, g.sink);
-  if (lo < s_hi) {
-    h_lo = lo;
-    h_hi = s_hi;
-  }
-  const int w_lo = max(lo, qa - g.window + 1);
-  if (w_lo < a_hi) {
-    h_lo = min(h_lo, w_lo);
-    h_hi = max(h_hi, a_hi);
-  }
-  if (h_hi < 0) {
-    hi = lo;
+  const int s_hi = min(a_hi, g.sink);               // sink run [lo, s_hi)
+  const int w_lo = max(lo, qa - g.window + 1);      // window run [w_lo, a_hi)
+  const bool has_s = lo < s_hi, has_w = w_lo < a_hi;
+  if (has_s && has_w && w_lo <= s_hi) {             // they touch: one run
+    hi1 = max(s_hi, a_hi);
+  } else if (has_s) {
+    hi1 = s_hi;
+    if (has_w) {
+      lo2 = w_lo;
+      hi2 = a_hi;
+    }
+  } else if (has_w) {
+    lo1 = w_lo;
+    hi1 = a_hi;
   } else {
-    lo = h_lo;
-    hi = h_hi;
+    hi1 = lo;                                       // nothing visible
   }
 }
 
@@ -68,13 +74,13 @@ __global__ __launch_bounds__(256) void decode_tokens_kernel(Geom g, const int32_
   __syncthreads();
   for (int c = 0; c < n_ent; c += 256) {
     const int e = c + threadIdx.x;
-    int lo = 0, hi = 0, flag = 0;
+    int lo1 = 0, hi1 = 0, lo2 = 0, hi2 = 0, flag = 0;
     if (e < n_ent) {
       const int ent = list[e];
-      tile_hull(g, ent & kIdxMask, lo, hi);
+      tile_runs(g, ent & kIdxMask, lo1, hi1, lo2, hi2);
       flag = (ent >> kPartialBit) & 1;
     }
-    const int len = hi - lo;
+    const int len1 = hi1 - lo1, len = len1 + (hi2 - lo2);
     int inc = len;
     for (int off = 1; off < 64; off <<= 1) {
       const int u = __shfl_up(inc, off);
@@ -85,7 +91,8 @@ __global__ __launch_bounds__(256) void decode_tokens_kernel(Geom g, const int32_
     int start = carry;
     for (int w = 0; w < wave; ++w) start += red[w];
     start += inc - len;
-    for (int t = 0; t < len; ++t) tok[start + t] = (lo + t) | (flag << kPartialBit);
+    for (int t = 0; t < len; ++t)
+      tok[start + t] = (t < len1 ? lo1 + t : lo2 + (t - len1)) | (flag << kPartialBit);
     __syncthreads();
     if (threadIdx.x == 0) carry += red[0] + red[1] + red[2] + red[3];
     __syncthreads();
@@ -187,7 +194,11 @@ struct DecodeQ<F32, NQ> {
 
 // Row r of the workgroup is query row qrow[r] (qrow = n_q marks an unused row,
 // which elem_valid rejects).
-template <typename T, int D, int NQ, int NU>
+// EXACT: every row sits at the same position (n_q == 1) and the stream holds
+// exactly the positions it can see, so a token is valid unless it is padding
+// or its tile's block-mask entry (partial tiles only) drops it -- one test per
+// token instead of the token rule per (row, token).
+template <typename T, int D, int NQ, int NU, bool EXACT>
 __device__ inline void decode_consume(const Geom& g, const DecodeRound<T, D, NU>& rd,
                                       const int (&qrow)[NQ], const DecodeQ<T, NQ>& qv,
                                       float (&m)[NQ], float (&l)[NQ],
@@ -198,12 +209,19 @@ __device__ inline void decode_consume(const Geom& g, const DecodeRound<T, D, NU>
   float sc[NQ][NU];
 #pragma unroll
   for (int u = 0; u < NU; ++u) {
+    bool ok_u = rd.pj[u] >= 0;                // sign bit: padding row of the round
+    if constexpr (EXACT) {
+      if (ok_u && ((rd.pj[u] >> kPartialBit) & 1))
+        ok_u = g.mask[(size_t)((g.n_q - 1) / g.bm) * g.n_kb + (rd.pj[u] & kIdxMask) / g.bn] != 0;
+    }
 #pragma unroll
     for (int r = 0; r < NQ; ++r) {
       float part = qv.dot(r, rd.kr[u]);
       part = group_sum<LPT>(part);             // the LPT lanes of a token row
-      bool ok = rd.pj[u] >= 0;                 // sign bit: padding row of the round
-      if (ok) ok = elem_valid(g, qrow[r], rd.pj[u] & kIdxMask, (rd.pj[u] >> kPartialBit) & 1);
+      bool ok = ok_u;
+      if constexpr (!EXACT) {
+        if (ok) ok = elem_valid(g, qrow[r], rd.pj[u] & kIdxMask, (rd.pj[u] >> kPartialBit) & 1);
+      }
       sc[r][u] = ok ? part * g.scale_log2 : kNegInf;
     }
   }
@@ -240,7 +258,7 @@ __device__ inline void decode_consume(const Geom& g, const DecodeRound<T, D, NU>
 // head (gq = group when group * n_q <= kDecodeMaxQ, else 1): its n_rows =
 // gq * n_q rows are rows bhq0 * n_q + r of Q / O / LSE, r = head * n_q + query
 // row, and share every K / V load.
-template <typename T, int D, int NQ, typename Src>
+template <typename T, int D, int NQ, typename Src, bool EXACT>
 __global__ __launch_bounds__(64 * decode_waves<NQ>()) void decode_kernel(
     Geom g, const typename T::storage* __restrict__ Q, const typename T::storage* __restrict__ K,
     const typename T::storage* __restrict__ V, typename T::storage* __restrict__ O,
@@ -302,13 +320,13 @@ __global__ __launch_bounds__(64 * decode_waves<NQ>()) void decode_kernel(
         R::positions(src, t0 + 2 * RT, w1, tk, pa);
         rb.fetch(src, pb, ch, K, V, kb);
       }
-      decode_consume<T, D, NQ, NU>(g, ra, qrow, qv, m, l, acc);
+      decode_consume<T, D, NQ, NU, EXACT>(g, ra, qrow, qv, m, l, acc);
       if (!has_b) break;
       if (t0 + 2 * RT < w1) {
         R::positions(src, t0 + 3 * RT, w1, tk, pb);
         ra.fetch(src, pa, ch, K, V, kb);
       }
-      decode_consume<T, D, NQ, NU>(g, rb, qrow, qv, m, l, acc);
+      decode_consume<T, D, NQ, NU, EXACT>(g, rb, qrow, qv, m, l, acc);
     }
   }
   // merge the token-row groups of the wave (same m), then the four waves
@@ -400,9 +418,16 @@ int launch_decode_t(const Geom& g, const void* q, const void* k, const void* v, 
                     hipStream_t stream, const char* what) {
   using S = typename T::storage;
   const int n_wgh = g.B * g.H / gq, n_rows = gq * g.n_q;
-  hipLaunchKernelGGL((decode_kernel<T, D, NQ, Src>), dim3(n_wgh * n_splits), dim3(64 * decode_waves<NQ>()), 0,
-                     stream, g, (const S*)q, (const S*)k, (const S*)v, (S*)o, lse, ws, src, kv_rows,
-                     n_tokens, n_splits, gq);
+  // one query position (always so for a single-row workgroup): the stream is
+  // exact for every row
+  if (NQ == 1 || g.n_q == 1)
+    hipLaunchKernelGGL((decode_kernel<T, D, NQ, Src, true>), dim3(n_wgh * n_splits),
+                       dim3(64 * decode_waves<NQ>()), 0, stream, g, (const S*)q, (const S*)k,
+                       (const S*)v, (S*)o, lse, ws, src, kv_rows, n_tokens, n_splits, gq);
+  else if constexpr (NQ > 1)
+    hipLaunchKernelGGL((decode_kernel<T, D, NQ, Src, false>), dim3(n_wgh * n_splits),
+                       dim3(64 * decode_waves<NQ>()), 0, stream, g, (const S*)q, (const S*)k,
+                       (const S*)v, (S*)o, lse, ws, src, kv_rows, n_tokens, n_splits, gq);
   if (n_splits > 1)
     hipLaunchKernelGGL((combine_kernel<T, D>), dim3(n_wgh * n_rows), dim3(64), 0, stream, ws, (S*)o, lse,
                        n_rows, n_splits);

@@ -126,9 +126,9 @@ int64_t gki_bsa_decode_workspace_floats(int32_t B, int32_t H, int32_t n_q,
 
 /* Decode token stream (once per mask): expands the kept kv tiles of the single
  * decode q tile (`tile_list`, n_tiles entries of the decode_tile_m x tile_n
- * schedule) into the positions of the tokens some query row can see (the hull
- * of each tile's sink prefix / window suffix / in-bounds rows), entry =
- * position | partial << 30. `tokens` holds n_tiles * tile_n int32; the count
+ * schedule) into exactly the positions some query row can see (per tile its
+ * sink run and its window run under the token rule; every in-bounds position
+ * when not causal), ascending, entry = position | partial << 30. `tokens` holds n_tiles * tile_n int32; the count
  * is written to the device scalar `n_tokens`. No reference counterpart: the
  * reference visits whole tiles (sparse_triton_kernel.py:283-299). */
 int gki_decode_tokens(const int32_t* tile_list, int32_t n_tiles, int32_t n_q, int32_t n_kv,

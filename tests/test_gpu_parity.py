@@ -138,6 +138,30 @@ def test_decode_schedule_matches_oracle():
                                   list(range(4)) + list(range(100000 - 2048, 100000)))
 
 
+@pytest.mark.parametrize("n_q,n_kv,sink,window,bm,bn", [
+    (1, 100, 4, 64, 1, 64),      # window starts inside tile 0, past the sinks
+    (1, 90, 4, 50, 1, 64),
+    (3, 500, 4, 100, 1, 64),
+    (4, 129, 2, 32, 2, 32),
+    (1, 1000, 0, 64, 1, 64),
+    (2, 300, 4, 0, 1, 64),       # W = 0: sinks only
+    (1, 3000, 4, 256, 1, 16),
+])
+def test_decode_stream_is_the_visible_union(n_q, n_kv, sink, window, bm, bn):
+    """The decode token stream is exactly the positions some query row can see
+    (ascending), except that for W = 0 and several rows it may keep the rows'
+    own positions, which the per-row token rule then drops."""
+    m = so.block_mask(n_q, n_kv, sink, window, bm, bn)
+    sched = decode_schedule(torch.from_numpy(m).to(DEV), n_q, n_kv, bm, bn, True, sink, window)
+    got = (sched.tokens.cpu().numpy() & ((1 << 30) - 1)).tolist()
+    assert got == sorted(got) and len(set(got)) == len(got)
+    vis = np.nonzero(so.token_mask(n_q, n_kv, sink, window).any(axis=0))[0].tolist()
+    if window >= 1 or n_q == 1:
+        assert got == vis
+    else:
+        assert set(vis) <= set(got) and set(got) - set(vis) <= set(range(n_kv - n_q + 1, n_kv))
+
+
 # ---------------------------------------------------------------------------
 # small shapes vs the fp64 oracle
 # ---------------------------------------------------------------------------
