@@ -163,6 +163,7 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
       t.store(sq[buf], tid);
       t.load(dO + qb, q0, g.n_q, tid);
       t.store(sdo[buf], tid);
+      dma_wait();   // nothing of this branch pending where it rejoins the DMA path
     }
     if (wave_u < 2) {
       const float* src = (wave_u == 0 ? LSE : Delta) + (size_t)bhq * g.n_q + min(q0 + lane, g.n_q - 1);
@@ -426,6 +427,7 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_16(
       t.store(sk[buf], tid);
       t.load(V + kb, k0, g.n_kv, tid);
       t.store(sv[buf], tid);
+      dma_wait();   // nothing of this branch pending where it rejoins the DMA path
     }
   };
   if (e_beg < e_end) stage((row_idx[e_beg] & kIdxMask) * kTileN, 0);

@@ -90,6 +90,10 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel_16(
       t.store(sk[b], tid);
       t.load(V + kb, k0, g.n_kv, tid);
       t.store(sv[b], tid);
+      // Unconditional, so that no register load of this branch is pending
+      // where it rejoins the DMA path: otherwise the compiler waits for all
+      // vector memory there, the just-issued DMA of the next tile included.
+      dma_wait();
     }
   };
 
