@@ -216,11 +216,23 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
       const float dv4[4] = {dlt4.x, dlt4.y, dlt4.z, dlt4.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], g.scale_log2, -lv[i]));
-        if (need_mask && !elem_valid(g, q0 + qr0 + i, my_kv, partial)) pv = 0.f;
+        const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], g.scale_log2, -lv[i]));
         p[t][i] = pv;
         ds[t][i] = pv * (dp[i] - dv4[i]) * g.scale;
       }
+    }
+    // Masked elements: P = dS = 0 (a bit select, so an exp that overflowed on
+    // an invisible element cannot leak). One uniform branch per tile keeps the
+    // selects off the tiles that need no mask.
+    if (need_mask) {
+      const LaneBits vis(col_valid_bits(g, my_kv, q0, partial), grp);
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          p[t][i] = vis.pick(t, i, p[t][i], 0.f);
+          ds[t][i] = vis.pick(t, i, ds[t][i], 0.f);
+        }
     }
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
@@ -461,10 +473,16 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_16(
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], g.scale_log2, -lse2));
-        if (need_mask && !elem_valid(g, my_q, k0 + rho(t, 4 * grp + i), partial)) pv = 0.f;
+        const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], g.scale_log2, -lse2));
         ds[t][i] = pv * (dp[i] - dlt) * g.scale;
       }
+    }
+    if (need_mask) {     // masked elements: dS = 0 (bit select, as in the dK/dV kernel)
+      const LaneBits vis(row_valid_bits(g, my_q, k0, partial), grp);
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ds[t][i] = vis.pick(t, i, ds[t][i], 0.f);
     }
 #pragma unroll
     for (int st = 0; st < 2; ++st) {

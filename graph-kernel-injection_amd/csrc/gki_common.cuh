@@ -315,7 +315,7 @@ __device__ inline bool token_visible(int q_abs, int k, int sink, int window) {
 }
 
 // Bounds + token predicate for (q row, kv column), branch-free.
-__device__ inline bool elem_tok(const Geom& g, int q_row, int kv) {
+__host__ __device__ inline bool elem_tok(const Geom& g, int q_row, int kv) {
   const int qa = q_row + g.q_off;
   const bool in = (q_row < g.n_q) & (kv < g.n_kv);
   const bool vis = (kv <= qa) & ((kv < g.sink) | (kv >= qa - g.window + 1));
@@ -324,11 +324,83 @@ __device__ inline bool elem_tok(const Geom& g, int q_row, int kv) {
 
 // Full element predicate for (q row, kv column) of a tile flagged "needs mask":
 // tiles flagged partial also consult the lifted block mask.
-__device__ inline bool elem_valid(const Geom& g, int q_row, int kv, bool partial) {
+__host__ __device__ inline bool elem_valid(const Geom& g, int q_row, int kv, bool partial) {
   bool ok = elem_tok(g, q_row, kv);
   if (partial && ok) ok = g.mask[(size_t)(q_row / g.bm) * g.n_kb + kv / g.bn] != 0;
   return ok;
 }
+
+// ---------------------------------------------------------------------------
+// The same predicate for 64 elements at once: one query row against the 64
+// keys of a tile (or one key against the 64 query rows of a tile) as a 64-bit
+// word, bit j = element j. The token rule is an interval condition along
+// either axis, so the word costs a few shifts per lane and tile instead of a
+// compare chain per element.
+// ---------------------------------------------------------------------------
+
+// Bits lo .. hi of a 64-bit word (clamped to 0 .. 63; empty when hi < lo).
+__host__ __device__ inline uint64_t bit_range(long lo, long hi) {
+  lo = lo < 0 ? 0 : lo;
+  hi = hi > 63 ? 63 : hi;
+  if (hi < lo) return 0;
+  const uint64_t upto = hi == 63 ? ~0ull : ((2ull << hi) - 1);
+  return upto & (~0ull << lo);
+}
+
+// elem_valid(g, q_row, k0 + j, partial) for j = 0 .. 63, as bits.
+__host__ __device__ inline uint64_t row_valid_bits(const Geom& g, int q_row, int k0, bool partial) {
+  if (q_row >= g.n_q) return 0;
+  uint64_t b = bit_range(0, (long)g.n_kv - 1 - k0);
+  if (g.causal) {
+    const long qa = (long)q_row + g.q_off - k0;   // key j visible iff j <= qa and
+    b &= bit_range(0, qa) &                        // (j >= qa - W + 1 or k0 + j < S)
+         (bit_range(qa - g.window + 1, 63) | bit_range(0, (long)g.sink - 1 - k0));
+  }
+  if (partial) {                                 // kept blocks of the row's block row
+    const int32_t* mrow = g.mask + (size_t)(q_row / g.bm) * g.n_kb;
+    uint64_t kept = 0;
+    for (int kb = k0 / g.bn; kb < g.n_kb && kb * g.bn < k0 + 64; ++kb)
+      if (mrow[kb]) kept |= bit_range((long)kb * g.bn - k0, (long)(kb + 1) * g.bn - 1 - k0);
+    b &= kept;
+  }
+  return b;
+}
+
+// elem_valid(g, q0 + j, kv, partial) for j = 0 .. 63, as bits.
+__host__ __device__ inline uint64_t col_valid_bits(const Geom& g, int kv, int q0, bool partial) {
+  if (kv >= g.n_kv) return 0;
+  uint64_t b = bit_range(0, (long)g.n_q - 1 - q0);
+  if (g.causal) {
+    const long a = (long)kv - g.q_off - q0;       // row j visible iff j >= a and
+    b &= bit_range(a, 63) &                        // (kv < S or j <= a + W - 1)
+         (kv < g.sink ? ~0ull : bit_range(0, a + g.window - 1));
+  }
+  if (partial) {                                 // kept blocks of the key's block column
+    const int kb = kv / g.bn;
+    uint64_t kept = 0;
+    for (int qb = q0 / g.bm; qb < g.n_qb && qb * g.bm < q0 + 64; ++qb)
+      if (g.mask[(size_t)qb * g.n_kb + kb]) kept |= bit_range((long)qb * g.bm - q0, (long)(qb + 1) * g.bm - 1 - q0);
+    b &= kept;
+  }
+  return b;
+}
+
+// The 16 elements that lane group `grp` holds in the rho() layout: element
+// (t, i) is tile row / key rho(t, 4 grp + i) = 32 (t >> 1) + 8 grp + 4 (t & 1) + i,
+// i.e. bit 4 (t & 1) + i of byte `grp` of word half t >> 1. Returned as two
+// words whose low 8 bits are those bytes.
+struct LaneBits {
+  uint32_t w[2];
+  __device__ inline LaneBits(uint64_t bits, int grp) {
+    w[0] = (uint32_t)bits >> (8 * grp);
+    w[1] = (uint32_t)(bits >> 32) >> (8 * grp);
+  }
+  // x where element (t, i) is set, `other` where it is not (bit-select, no compare)
+  __device__ inline float pick(int t, int i, float x, float other) const {
+    const int m = __builtin_amdgcn_sbfe((int)w[t >> 1], 4 * (t & 1) + i, 1);   // 0 or -1
+    return __int_as_float((__float_as_int(x) & m) | (__float_as_int(other) & ~m));
+  }
+};
 
 // Is some (q, k) with q in [q_lo, q_hi], k in [k_lo, k_hi] (inclusive, absolute
 // positions, non-empty) visible under the token rule (k <= q) & (k < S | k >= q-W+1)?

@@ -131,12 +131,11 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel_16(
       const bool need_mask = partial || (q0 + 15 >= g.n_q) || (k0 + kTileN > g.n_kv) ||
                              !tile_all_visible(g, q0, min(q0 + 15, g.n_q - 1), k0, k0 + kTileN - 1);
       if (need_mask) {
-        const int my_q = q0 + col;
+        const LaneBits vis(row_valid_bits(g, q0 + col, k0, partial), grp);
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (!elem_valid(g, my_q, k0 + rho(t, 4 * grp + i), partial)) s[h][t][i] = kNegInf;
+          for (int i = 0; i < 4; ++i) s[h][t][i] = vis.pick(t, i, s[h][t][i], kNegInf);
       }
       float mx = kNegInf;
 #pragma unroll
