@@ -339,28 +339,33 @@ __host__ __device__ inline bool elem_valid(const Geom& g, int q_row, int kv, boo
 // ---------------------------------------------------------------------------
 
 // Bits lo .. hi of a 64-bit word (clamped to 0 .. 63; empty when hi < lo).
-__host__ __device__ inline uint64_t bit_range(long lo, long hi) {
+__host__ __device__ inline uint64_t bit_range(int lo, int hi) {
   lo = lo < 0 ? 0 : lo;
   hi = hi > 63 ? 63 : hi;
-  if (hi < lo) return 0;
-  const uint64_t upto = hi == 63 ? ~0ull : ((2ull << hi) - 1);
-  return upto & (~0ull << lo);
+  return hi < lo ? 0 : (~0ull >> (63 - hi)) & (~0ull << lo);
+}
+
+// Window length for the visibility words: any window of at least n_kv keys
+// reaches key 0 from every row, so clamping there is exact and keeps the
+// window-edge arithmetic inside int for n_q, n_kv < 2^30.
+__host__ __device__ inline int word_window(const Geom& g) {
+  return g.window < g.n_kv ? g.window : g.n_kv;
 }
 
 // elem_valid(g, q_row, k0 + j, partial) for j = 0 .. 63, as bits.
 __host__ __device__ inline uint64_t row_valid_bits(const Geom& g, int q_row, int k0, bool partial) {
   if (q_row >= g.n_q) return 0;
-  uint64_t b = bit_range(0, (long)g.n_kv - 1 - k0);
+  uint64_t b = bit_range(0, g.n_kv - 1 - k0);
   if (g.causal) {
-    const long qa = (long)q_row + g.q_off - k0;   // key j visible iff j <= qa and
+    const int qa = q_row + g.q_off - k0;           // key j visible iff j <= qa and
     b &= bit_range(0, qa) &                        // (j >= qa - W + 1 or k0 + j < S)
-         (bit_range(qa - g.window + 1, 63) | bit_range(0, (long)g.sink - 1 - k0));
+         (bit_range(qa - word_window(g) + 1, 63) | bit_range(0, g.sink - 1 - k0));
   }
   if (partial) {                                 // kept blocks of the row's block row
     const int32_t* mrow = g.mask + (size_t)(q_row / g.bm) * g.n_kb;
     uint64_t kept = 0;
     for (int kb = k0 / g.bn; kb < g.n_kb && kb * g.bn < k0 + 64; ++kb)
-      if (mrow[kb]) kept |= bit_range((long)kb * g.bn - k0, (long)(kb + 1) * g.bn - 1 - k0);
+      if (mrow[kb]) kept |= bit_range(kb * g.bn - k0, (kb + 1) * g.bn - 1 - k0);
     b &= kept;
   }
   return b;
@@ -369,17 +374,17 @@ __host__ __device__ inline uint64_t row_valid_bits(const Geom& g, int q_row, int
 // elem_valid(g, q0 + j, kv, partial) for j = 0 .. 63, as bits.
 __host__ __device__ inline uint64_t col_valid_bits(const Geom& g, int kv, int q0, bool partial) {
   if (kv >= g.n_kv) return 0;
-  uint64_t b = bit_range(0, (long)g.n_q - 1 - q0);
+  uint64_t b = bit_range(0, g.n_q - 1 - q0);
   if (g.causal) {
-    const long a = (long)kv - g.q_off - q0;       // row j visible iff j >= a and
+    const int a = kv - g.q_off - q0;               // row j visible iff j >= a and
     b &= bit_range(a, 63) &                        // (kv < S or j <= a + W - 1)
-         (kv < g.sink ? ~0ull : bit_range(0, a + g.window - 1));
+         (kv < g.sink ? ~0ull : bit_range(0, a + word_window(g) - 1));
   }
   if (partial) {                                 // kept blocks of the key's block column
     const int kb = kv / g.bn;
     uint64_t kept = 0;
     for (int qb = q0 / g.bm; qb < g.n_qb && qb * g.bm < q0 + 64; ++qb)
-      if (g.mask[(size_t)qb * g.n_kb + kb]) kept |= bit_range((long)qb * g.bm - q0, (long)(qb + 1) * g.bm - 1 - q0);
+      if (g.mask[(size_t)qb * g.n_kb + kb]) kept |= bit_range(qb * g.bm - q0, (qb + 1) * g.bm - 1 - q0);
     b &= kept;
   }
   return b;
