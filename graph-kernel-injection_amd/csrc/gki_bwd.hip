@@ -390,8 +390,8 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_32(
 template <typename T, int D>
 __global__ __launch_bounds__(256, 2) void dq_kernel_16(
     Geom g, const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
-    const uint16_t* __restrict__ V, const uint16_t* __restrict__ dO, uint16_t* __restrict__ dQ,
-    const float* __restrict__ LSE, const float* __restrict__ Delta,
+    const uint16_t* __restrict__ V, const uint16_t* __restrict__ O, const uint16_t* __restrict__ dO,
+    uint16_t* __restrict__ dQ, const float* __restrict__ LSE, float* __restrict__ Delta,
     const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ row_idx, int n_qt) {
   constexpr int KS = (D + 31) / 32;
   constexpr int DT = D / 16;
@@ -418,7 +418,25 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_16(
     df[ks] = ok ? *(const uint4*)(dO + qb + (size_t)my_q * D + d0) : make_uint4(0, 0, 0, 0);
   }
   const float lse2 = my_q < g.n_q ? LSE[(size_t)bh * g.n_q + my_q] * kLog2e : 0.f;
-  const float dlt = my_q < g.n_q ? Delta[(size_t)bh * g.n_q + my_q] : 0.f;
+  // Delta = rowsum(O * dO) in fp32 over the stored O (the preprocessing pass,
+  // sparse_triton_kernel.py:354-392, fused here): the lane already holds its
+  // row's dO chunks, the four lane groups of a row are summed across. Every q
+  // row has exactly one dQ workgroup, which writes it for the dK/dV kernel
+  // that runs next.
+  float part = 0.f;
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const int d0 = 32 * ks + 8 * grp;
+    if (my_q < g.n_q && d0 < D) {
+      const uint4 o4 = *(const uint4*)(O + qb + (size_t)my_q * D + d0);
+      const uint16_t* ho = (const uint16_t*)&o4;
+      const uint16_t* hd = (const uint16_t*)&df[ks];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) part += T::to_float(ho[i]) * T::to_float(hd[i]);
+    }
+  }
+  const float dlt = wave_sum16x4(part);
+  if (my_q < g.n_q && grp == 0) Delta[(size_t)bh * g.n_q + my_q] = dlt;
 
   floatx4 dq[DT];
 #pragma unroll
@@ -626,23 +644,25 @@ int launch_bwd(int dtype, const Geom& g, const void* q, const void* k, const voi
                        (const float*)k, (const float*)v, (const float*)dout, (float*)dq, lse, delta,
                        row_ptr, row_idx, n_qt);
   } else if (dtype == kF16) {
-    launch_delta<F16, D>(o, dout, delta, rows, stream);
+    // dQ first: it also produces Delta, which dK/dV reads
+    hipLaunchKernelGGL((dq_kernel_16<F16, D>), dim3(n_qt * BH), dim3(256), 0, stream, g,
+                       (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
+                       (const uint16_t*)o, (const uint16_t*)dout, (uint16_t*)dq, lse, delta,
+                       row_ptr, row_idx, n_qt);
     hipLaunchKernelGGL((dkdv_kernel_16<F16, D>), dim3(n_kt * BHkv), dim3(256), 0, stream, g,
                        (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
                        (const uint16_t*)dout, (uint16_t*)dk, (uint16_t*)dv, lse, delta, col_ptr,
                        col_idx, order, n_heavy, n_kt);
-    hipLaunchKernelGGL((dq_kernel_16<F16, D>), dim3(n_qt * BH), dim3(256), 0, stream, g,
-                       (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
-                       (const uint16_t*)dout, (uint16_t*)dq, lse, delta, row_ptr, row_idx, n_qt);
   } else {
-    launch_delta<BF16, D>(o, dout, delta, rows, stream);
+    // dQ first: it also produces Delta, which dK/dV reads
+    hipLaunchKernelGGL((dq_kernel_16<BF16, D>), dim3(n_qt * BH), dim3(256), 0, stream, g,
+                       (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
+                       (const uint16_t*)o, (const uint16_t*)dout, (uint16_t*)dq, lse, delta,
+                       row_ptr, row_idx, n_qt);
     hipLaunchKernelGGL((dkdv_kernel_16<BF16, D>), dim3(n_kt * BHkv), dim3(256), 0, stream, g,
                        (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
                        (const uint16_t*)dout, (uint16_t*)dk, (uint16_t*)dv, lse, delta, col_ptr,
                        col_idx, order, n_heavy, n_kt);
-    hipLaunchKernelGGL((dq_kernel_16<BF16, D>), dim3(n_qt * BH), dim3(256), 0, stream, g,
-                       (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
-                       (const uint16_t*)dout, (uint16_t*)dq, lse, delta, row_ptr, row_idx, n_qt);
   }
   return check_launch("gki_bsa_bwd");
 }
