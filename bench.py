@@ -101,6 +101,29 @@ def _time_calls(fn, steps: int, warmup: int):
     return per_step, [a.elapsed_time(b) for a, b in evs]
 
 
+def _time_cold(fn, calls: int = 40):
+    """Per-call time of ``fn`` with the device's last-level (Infinity) cache
+    evicted first: a 2 GiB read runs before each timed call (outside its
+    events, so the call is queued behind it and no host gap is timed). Back-to-
+    back decode steps re-read the same rows, which a 256 MB memory-side cache
+    can partly hold; this is the same step with HBM serving all of them.
+    Returns the median ms per call."""
+    import torch
+
+    flush = torch.empty(2 << 30, dtype=torch.uint8, device="cuda:0").view(torch.int64)
+    times = []
+    for _ in range(calls):
+        flush.sum()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        fn()
+        b.record()
+        torch.cuda.synchronize()
+        times.append(a.elapsed_time(b))
+    del flush
+    return statistics.median(times)
+
+
 def _traffic(*keys: str):
     """HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE (scaled
     by a plain copy of known size), summed over the named kernels; from
@@ -231,6 +254,13 @@ def section_c4(steps: int, warmup: int) -> dict:
     res["roofline"] = _roofline(gbs, PEAK_HBM, "GB/s", "hbm", _traffic("c4_decode"))
     log(f"[c4] decode step {avg * 1e3:.2f} us, {gbs:.0f} GB/s token-exact "
         f"({100 * gbs / PEAK_HBM:.1f}% of HBM peak)")
+    cold = _time_cold(fn)
+    res["cold_cache"] = {"per_call_ms": cold, "kv_gbs": exact_bytes / (cold * 1e-3) / 1e9,
+                         "frac": exact_bytes / (cold * 1e-3) / 1e9 / PEAK_HBM,
+                         "protocol": "median of 40 calls, each after a 2 GiB read that evicts "
+                                     "the 256 MB memory-side cache"}
+    log(f"[c4] decode step after evicting the memory-side cache: {cold * 1e3:.2f} us, "
+        f"{res['cold_cache']['kv_gbs']:.0f} GB/s ({100 * res['cold_cache']['frac']:.1f}% of HBM peak)")
     res["rolling_cache"] = _rolling_c4(q, k, v, S, W, fn(), exact_bytes, steps, warmup)
     del k, v
     res["gqa"] = _gqa_c4(B, H, NKV, D, S, W, mask, steps, warmup)
