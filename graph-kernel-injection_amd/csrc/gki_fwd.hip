@@ -142,9 +142,12 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel_16(
       for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[h][t][i]);
-      mx = wave_max16x4(mx) * g.scale_log2;     // softmax_scale > 0 (checked on the host)
-      const bool grow = mx > m[h] + kRescaleSlack;
-      if (__any(grow)) {
+      // A row's max exceeds the reference by the slack only if one of its
+      // lanes' maxima does (softmax_scale > 0, checked on the host, so scaling
+      // after the max is exact): the cross-lane reduction runs only then.
+      if (__any(mx * g.scale_log2 > m[h] + kRescaleSlack)) {
+        mx = wave_max16x4(mx) * g.scale_log2;
+        const bool grow = mx > m[h] + kRescaleSlack;
         const float alpha = grow ? __builtin_amdgcn_exp2f(m[h] - mx) : 1.f;
         m[h] = grow ? mx : m[h];
         lsum[h][0] *= alpha;
