@@ -30,6 +30,9 @@
 namespace gki {
 namespace {
 
+// Slack of the decode's lazy reference max, in log2 units: p = exp2(s - m) <= 2^8.
+constexpr float kDecodeSlack = 8.f;
+
 
 // The tokens of kv tile `kt` that some of the n_q rows can see, as at most two
 // ascending runs [lo1, hi1), [lo2, hi2): the sink run and the window run (one
@@ -230,14 +233,22 @@ __device__ inline void decode_consume(const Geom& g, const DecodeRound<T, D, NU>
     float mx = kNegInf;
 #pragma unroll
     for (int u = 0; u < NU; ++u) mx = fmaxf(mx, sc[r][u]);
-    mx = cross_group_max<LPT>(mx);             // scores are uniform within a token row
-    const float m_new = fmaxf(m[r], mx);
-    const float mu = m_new == kNegInf ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m[r] - mu);
-    m[r] = m_new;
-    float rs = 0.f;
+    // Lazy reference max (wave-uniform): it moves, to the exact running max,
+    // only when some score of the round exceeds it by the slack, so p stays
+    // below 2^slack and the rescale (a cross-lane max, one exp2, VEC + 1
+    // multiplies) is skipped in almost every round. acc / l is exact for any
+    // reference max.
+    if (__any(mx > m[r] + kDecodeSlack)) {
+      mx = cross_group_max<LPT>(mx);           // scores are uniform within a token row
+      const float m_new = fmaxf(m[r], mx);
+      const float alpha = __builtin_amdgcn_exp2f(m[r] - m_new);   // m = -inf: 0
+      m[r] = m_new;
+      l[r] *= alpha;
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) acc[r][i] *= alpha;
+      for (int i = 0; i < VEC; ++i) acc[r][i] *= alpha;
+    }
+    const float mu = m[r] == kNegInf ? 0.f : m[r];
+    float rs = 0.f;
 #pragma unroll
     for (int u = 0; u < NU; ++u) {
       const float p = __builtin_amdgcn_exp2f(sc[r][u] - mu);
@@ -249,7 +260,7 @@ __device__ inline void decode_consume(const Geom& g, const DecodeRound<T, D, NU>
 #pragma unroll
       for (int i = 0; i < VEC; ++i) acc[r][i] += pv * T::to_float(e[i]);
     }
-    l[r] = l[r] * alpha + rs;
+    l[r] += rs;
   }
 }
 
