@@ -2,8 +2,10 @@
 //
 // Replaces the reference's three Triton launches in
 // `_BlockSparseFlashAttention.backward` (sparse_triton_kernel.py:719-777):
-//   * delta_kernel  <- `_bwd_preprocess_kernel` (sparse_triton_kernel.py:354-392):
-//       Delta[q] = sum_d fp32(O) * fp32(dO), using the stored O.
+//   * `_bwd_preprocess_kernel` (sparse_triton_kernel.py:354-392),
+//       Delta[q] = sum_d fp32(O) * fp32(dO) over the stored O: for 16-bit
+//       inputs inside dq_kernel_16, which runs first and stores Delta * scale
+//       for dK/dV; for fp32 inputs delta_kernel, before the other two.
 //   * dkdv_kernel   <- `_bwd_dkdv_kernel` (sparse_triton_kernel.py:394-509):
 //       one workgroup per 64-row KV tile, loop over the kept q tiles of its
 //       column (CSC list), P = exp(S - LSE), dV += P^T dO, dS = P (dP - Delta)
@@ -218,7 +220,7 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
       for (int i = 0; i < 4; ++i) {
         const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], g.scale_log2, -lv[i]));
         p[t][i] = pv;
-        ds[t][i] = pv * (dp[i] - dv4[i]) * g.scale;
+        ds[t][i] = pv * __builtin_fmaf(dp[i], g.scale, -dv4[i]);   // Delta * scale from dQ
       }
     }
     // Masked elements: P = dS = 0 (a bit select, so an exp that overflowed on
@@ -435,7 +437,8 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_16(
       for (int i = 0; i < 8; ++i) part += T::to_float(ho[i]) * T::to_float(hd[i]);
     }
   }
-  const float dlt = wave_sum16x4(part);
+  // stored and used pre-scaled: dS = P (dP scale - Delta scale), one fma
+  const float dlt = wave_sum16x4(part) * g.scale;
   if (my_q < g.n_q && grp == 0) Delta[(size_t)bh * g.n_q + my_q] = dlt;
 
   floatx4 dq[DT];
@@ -492,7 +495,7 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_16(
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], g.scale_log2, -lse2));
-        ds[t][i] = pv * (dp[i] - dlt) * g.scale;
+        ds[t][i] = pv * __builtin_fmaf(dp[i], g.scale, -dlt);
       }
     }
     if (need_mask) {     // masked elements: dS = 0 (bit select, as in the dK/dV kernel)

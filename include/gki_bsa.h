@@ -105,10 +105,12 @@ int gki_bsa_fwd(const void* q, const void* k, const void* v, void* o, float* lse
                 int32_t sink_size, int32_t window_size, void* stream);
 
 /* Backward: replaces the three launches in `_BlockSparseFlashAttention.backward`
- * (sparse_triton_kernel.py:719-777): Delta = rowsum(O * dO) into `delta`, then
- * dK/dV over the CSC list (kv_order / n_heavy from gki_heavy_order), then dQ
- * over the CSR list, both over bwd_tile_m x tile_n tiles. dq, dk, dv are fully
- * written (no zero-fill needed). */
+ * (sparse_triton_kernel.py:719-777): the row terms Delta = rowsum(O * dO), dK/dV
+ * over the CSC list (kv_order / n_heavy from gki_heavy_order) and dQ over the
+ * CSR list, both over bwd_tile_m x tile_n tiles. `delta` is a caller-owned fp32
+ * [B, H, N_Q] workspace for the row terms (its contents on return are internal:
+ * Delta for fp32 inputs, Delta * softmax_scale for fp16 / bf16). dq, dk, dv are
+ * fully written (no zero-fill needed). */
 int gki_bsa_bwd(const void* q, const void* k, const void* v, const void* o,
                 const void* dout, const float* lse, void* dq, void* dk, void* dv,
                 float* delta, int32_t dtype, int32_t B, int32_t H, int32_t H_kv,
