@@ -309,11 +309,6 @@ __device__ inline int kv_bh(const Geom& g, int bh) {
   return g.group == 1 ? bh : (bh / g.H) * g.H_kv + (bh % g.H) / g.group;
 }
 
-// StreamingLLM token predicate on absolute positions (k <= q) & (k < S | k >= q-W+1).
-__device__ inline bool token_visible(int q_abs, int k, int sink, int window) {
-  return (k <= q_abs) && (k < sink || k >= q_abs - window + 1);
-}
-
 // Bounds + token predicate for (q row, kv column), branch-free.
 __host__ __device__ inline bool elem_tok(const Geom& g, int q_row, int kv) {
   const int qa = q_row + g.q_off;
