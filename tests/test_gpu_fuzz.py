@@ -1,0 +1,108 @@
+"""Seeded random sweep of the op against the fp64 oracle (GPU).
+
+Each case draws its own geometry: batch 1-2, grouped-query groups 1/2/4 over
+1-2 kv heads, n_kv 1..320 with n_q <= n_kv (a prefill offset) or occasionally
+n_q > n_kv, head_dim 16/32/64/128, block sizes from the reference's set,
+fp32 / fp16 / bf16, and either a StreamingLLM mask (random S, W, including 0)
+with the causal token rule or a random block mask with causal on or off
+(empty rows included). Forward and backward through
+``block_sparse_attention`` (n_q <= 4 takes the decode path) against the
+oracle's closed forms (sparse_triton_kernel.py:845-902 semantics).
+
+Inputs at the configs' scales (N(0,1) times 0.5 or 1) are held to the
+element-wise tolerances the parity tests use: fp32 atol 1e-5; fp16 / bf16
+atol 2e-2 + rtol 1e-2. Inputs times 2 (logits of standard deviation ~4,
+gradients ~20) are held to a magnitude-relative bound instead, relative
+Frobenius error <= 1e-5 (fp32) / 1e-2 (fp16, bf16): fixed absolute bounds do
+not scale with the values, and the kernels' error there is rounding-level
+(~1e-6 fp32, ~5e-3 bf16, where 16-bit P and dS are rounded as the reference
+rounds them).
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import sparse_triton_kernel as stk
+from oracle import streaming_oracle as so
+
+DEV = "cuda"
+TOL = {torch.float32: (1e-5, 0.0), torch.float16: (2e-2, 1e-2), torch.bfloat16: (2e-2, 1e-2)}
+REL = {torch.float32: 1e-5, torch.float16: 1e-2, torch.bfloat16: 1e-2}
+BLOCKS = [1, 2, 8, 16, 32, 64, 128]
+N_CASES = 96
+
+
+def _case(seed):
+    rng = np.random.default_rng(1000 + seed)
+    B = int(rng.integers(1, 3))
+    H_kv = int(rng.integers(1, 3))
+    group = int(rng.choice([1, 1, 2, 4]))
+    n_kv = int(rng.integers(1, 321))
+    n_q = int(rng.integers(1, n_kv + 1)) if rng.random() < 0.85 else int(rng.integers(n_kv, n_kv + 40))
+    if rng.random() < 0.2:
+        n_q = int(rng.integers(1, 5))                        # decode-sized
+    D = int(rng.choice([16, 32, 64, 128]))
+    dtype = [torch.float32, torch.float16, torch.bfloat16][int(rng.integers(0, 3))]
+    bm, bn = int(rng.choice(BLOCKS)), int(rng.choice(BLOCKS))
+    streaming = rng.random() < 0.7
+    causal = True if streaming else bool(rng.random() < 0.5)
+    sink = int(rng.integers(0, 9))
+    window = 0 if rng.random() < 0.1 else int(rng.integers(1, 400))
+    scale = float(rng.choice([0.5, 1.0, 2.0]))
+    return dict(B=B, H_kv=H_kv, group=group, n_q=n_q, n_kv=n_kv, D=D, dtype=dtype, bm=bm, bn=bn,
+                streaming=streaming, causal=causal, sink=sink, window=window, scale=scale,
+                mask_seed=int(rng.integers(0, 1 << 30)))
+
+
+def _close(ours, ref, dtype, what, elementwise):
+    o = ours.detach().to(torch.float64).cpu()
+    r = torch.as_tensor(ref).to(torch.float64)
+    assert torch.isfinite(o).all(), what
+    rel = ((o - r).norm() / r.norm().clamp_min(1e-30)).item() if r.abs().max() > 0 else o.abs().max().item()
+    info = f"max err {(o - r).abs().max():.3e}, max |ref| {r.abs().max():.3e}, relative Frobenius error {rel:.2e}"
+    if elementwise:
+        atol, rtol = TOL[dtype]
+        bad = (o - r).abs() > atol + rtol * r.abs()
+        assert not bad.any(), f"{what}: {int(bad.sum())} out of tolerance, {info}"
+    else:
+        assert rel <= REL[dtype], f"{what}: {info}"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(N_CASES))
+def test_random_case_matches_oracle(seed):
+    c = _case(seed)
+    print(f"[case] seed {seed}: {c}", flush=True)
+    B, H_kv, group, n_q, n_kv, D, dtype = (c[k] for k in ("B", "H_kv", "group", "n_q", "n_kv", "D", "dtype"))
+    H = H_kv * group
+    bm, bn, causal, sink, window = c["bm"], c["bn"], c["causal"], c["sink"], c["window"]
+    if c["streaming"]:
+        mask = stk.make_streaming_mask(n_q, n_kv, stk.StreamingMaskSpec(sink, window), bm, bn, device=DEV)
+    else:
+        mrng = np.random.default_rng(c["mask_seed"])
+        m = (mrng.random((-(-n_q // bm), -(-n_kv // bn))) < 0.6).astype(np.int32)
+        mask = torch.from_numpy(m).to(DEV)
+    gen = torch.Generator().manual_seed(seed)
+    mk = lambda *s: (torch.randn(*s, generator=gen) * c["scale"]).to(dtype).to(DEV)  # noqa: E731
+    q, k, v, do = mk(B, H, n_q, D), mk(B, H_kv, n_kv, D), mk(B, H_kv, n_kv, D), mk(B, H, n_q, D)
+    leaves = [t.clone().requires_grad_(True) for t in (q, k, v)]
+    out = stk.block_sparse_attention(*leaves, mask, block_m=bm, block_n=bn, is_causal=causal,
+                                     sink_size=sink, window_size=window, enable_gqa=group > 1)
+    out.backward(do)
+
+    eff = so.effective_mask(mask.cpu().numpy(), n_q, n_kv, bm, bn, causal, sink, window)
+    qn, kn, vn, don = (t.to(torch.float64).cpu().numpy() for t in (q, k, v, do))
+    kx, vx = so.expand_kv_heads(kn, group), so.expand_kv_heads(vn, group)
+    s = 1.0 / math.sqrt(D)
+    o_ref, _ = so.attention_fwd(qn, kx, vx, eff, s)
+    dq, dk, dv = so.attention_bwd(qn, kx, vx, don, eff, s)
+    tag, ew = f"seed {seed}", c["scale"] <= 1.0
+    _close(out, o_ref, dtype, "O " + tag, ew)
+    _close(leaves[0].grad, dq, dtype, "dQ " + tag, ew)
+    _close(leaves[1].grad, so.reduce_kv_grad(dk, group), dtype, "dK " + tag, ew)
+    _close(leaves[2].grad, so.reduce_kv_grad(dv, group), dtype, "dV " + tag, ew)
