@@ -23,6 +23,8 @@ the key. Building a schedule synchronises the stream once (to size the lists).
 
 from __future__ import annotations
 
+import ctypes
+
 import threading
 from collections import OrderedDict
 from dataclasses import dataclass
@@ -67,6 +69,12 @@ class DecodeSchedule:
     n_tiles: int
     tokens: torch.Tensor      # [n_tokens] int32 visible token positions (| partial << 30)
     n_tokens: int
+    # > 0 when the stream is exactly the causal StreamingLLM one of (n_kv, sink,
+    # window) -- the sinks, then the last positions any of the n_q rows can see --
+    # so the decode can compute it instead of reading the list: the full cache
+    # then decodes as a sink + ring cache with ring length n_kv - sink (slot =
+    # position). 0 otherwise (custom masks, partial tiles, short caches).
+    ring: int = 0
 
 
 def _stream(device: torch.device) -> int:
@@ -235,7 +243,19 @@ def decode_schedule(mask: torch.Tensor, n_q: int, n_kv: int, block_m: int, block
                                          int(bool(is_causal)), sink, window, tokens.data_ptr(),
                                          count.data_ptr(), _stream(mask.device)), "gki_decode_tokens")
         n_tokens = int(count.item())
-        return DecodeSchedule(lists.row_idx, lists.nnz, tokens[:n_tokens], n_tokens)
+        toks = tokens[:n_tokens]
+        ring = 0
+        r = n_kv - sink
+        if is_causal and r >= 1 and r >= window + n_q - 1 and n_kv < (1 << 30):
+            a, b, c = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+            _lib.check(lib.gki_rolling_stream(n_kv, n_q, sink, window, r, ctypes.byref(a),
+                                              ctypes.byref(b), ctypes.byref(c)), "gki_rolling_stream")
+            if c.value == n_tokens:
+                arith = torch.cat([torch.arange(a.value, dtype=torch.int32, device=mask.device),
+                                   torch.arange(b.value, n_kv, dtype=torch.int32, device=mask.device)])
+                if torch.equal(toks, arith):
+                    ring = r
+        return DecodeSchedule(lists.row_idx, lists.nnz, toks, n_tokens, ring)
 
     key = ("decode", n_q, n_kv, block_m, block_n, tm, tn, bool(is_causal), sink, window)
     return _CACHE.get(mask, key, build)

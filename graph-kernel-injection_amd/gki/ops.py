@@ -6,8 +6,10 @@ signatures, same validation order, exception types and messages, same saved
 state and gradient tuple. The Triton launches are replaced by calls into the
 C ABI of ``libgki_bsa.so`` on the caller's current HIP stream:
 
-* forward  -> ``gki_bsa_fwd`` (prefill) or ``gki_bsa_decode`` (n_q <= 4,
-  head_dim 64/128: the decode step),
+* forward  -> ``gki_bsa_fwd`` (prefill) or, for the decode step (n_q <= 4,
+  head_dim 64/128), ``gki_bsa_decode`` over the schedule's token list -- or
+  ``gki_rolling_decode`` over the full cache (ring length n_kv - sink) when that
+  list is the plain StreamingLLM stream, which the kernel then computes,
 * backward -> ``gki_bsa_bwd`` (Delta, dK/dV, dQ).
 
 There is no CPU or eager fallback: a missing library raises ``RuntimeError``.
@@ -138,10 +140,18 @@ class _BlockSparseFlashAttention(torch.autograd.Function):
                     ws = torch.empty(int(lib.gki_bsa_decode_workspace_floats(B, H, N_Q, D, n_splits)),
                                      dtype=torch.float32, device=dev)
                     ws_ptr = ws.data_ptr()
-                _lib.check(lib.gki_bsa_decode(
-                    q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), dtype,
-                    B, H, H_kv, N_Q, N_KV, D, sched.tokens.data_ptr(), sched.n_tokens, *common,
-                    ws_ptr, n_splits, stream), "gki_bsa_decode")
+                if sched.ring:
+                    # the stream is the StreamingLLM one: positions computed in
+                    # the kernel (no list read), same stream and arithmetic
+                    _lib.check(lib.gki_rolling_decode(
+                        q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                        dtype, B, H, H_kv, N_Q, D, int(sink_size), int(window_size), sched.ring,
+                        N_KV, float(softmax_scale), ws_ptr, n_splits, stream), "gki_rolling_decode")
+                else:
+                    _lib.check(lib.gki_bsa_decode(
+                        q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), dtype,
+                        B, H, H_kv, N_Q, N_KV, D, sched.tokens.data_ptr(), sched.n_tokens, *common,
+                        ws_ptr, n_splits, stream), "gki_bsa_decode")
             else:
                 sched = fwd_schedule(block_mask, N_Q, N_KV, block_m, block_n, bool(is_causal),
                                      int(sink_size), int(window_size), q.dtype == torch.float32)

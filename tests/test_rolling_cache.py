@@ -218,3 +218,46 @@ def test_rolling_decode_steps_across_the_ring_wrap():
     assert n_exact > steps // 2
     o_ref, _ = _oracle(q[:, :, -1:], k, v, sink, window)
     _close(o, o_ref, dtype, "last step vs oracle")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,H,H_kv,n_q,n_kv,D,S,W,dtype", [
+    (2, 4, 4, 1, 3000, 128, 4, 512, torch.bfloat16),
+    (1, 8, 2, 1, 5000, 128, 4, 1024, torch.bfloat16),   # grouped-query, 4 heads per stream
+    (2, 3, 3, 3, 700, 64, 2, 100, torch.float16),
+    (1, 4, 1, 2, 900, 64, 0, 200, torch.float32),
+])
+def test_full_cache_decode_computes_the_stream(B, H, H_kv, n_q, n_kv, D, S, W, dtype):
+    """A StreamingLLM mask's decode stream is computed in the kernel (the full
+    cache decoded as a sink + ring cache, slot = position) instead of read from
+    the token list; both give the same bits. A custom mask keeps the list."""
+    print(f"[case] B{B} H{H}/{H_kv} nq{n_q} nkv{n_kv} D{D} S{S} W{W} {dtype}", flush=True)
+    mask = stk.make_streaming_mask(n_q, n_kv, stk.StreamingMaskSpec(S, W), 1, 64, device=DEV)
+    sched = decode_schedule(mask, n_q, n_kv, 1, 64, True, S, W)
+    assert sched.ring == n_kv - S
+    g = torch.Generator().manual_seed(n_kv + n_q)
+    mk = lambda *s: torch.randn(*s, generator=g).to(dtype).to(DEV)  # noqa: E731
+    q, k, v = mk(B, H, n_q, D), mk(B, H_kv, n_kv, D), mk(B, H_kv, n_kv, D)
+    o = stk.block_sparse_attention(q, k, v, mask, block_m=1, block_n=64, is_causal=True,
+                                   sink_size=S, window_size=W, enable_gqa=H != H_kv)
+    # the token-list entry on the same schedule
+    from gki import ops
+    lib = _lib.load()
+    n_splits = ops._decode_splits(sched.n_tokens, ops._decode_slots(B, H, H_kv, n_q, 4))
+    ws = torch.empty(max(1, int(lib.gki_bsa_decode_workspace_floats(B, H, n_q, D, n_splits))),
+                     device=DEV)
+    o_list = torch.empty_like(q)
+    lse = torch.empty(B, H, n_q, device=DEV)
+    code = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}[dtype]
+    _lib.check(lib.gki_bsa_decode(q.data_ptr(), k.data_ptr(), v.data_ptr(), o_list.data_ptr(),
+                                  lse.data_ptr(), code, B, H, H_kv, n_q, n_kv, D,
+                                  sched.tokens.data_ptr(), sched.n_tokens, mask.data_ptr(),
+                                  mask.shape[0], mask.shape[1], 1, 64, 1.0 / math.sqrt(D), 1, S, W,
+                                  ws.data_ptr() if n_splits > 1 else 0, n_splits,
+                                  torch.cuda.current_stream().cuda_stream), "gki_bsa_decode")
+    torch.cuda.synchronize()
+    assert torch.equal(o, o_list)
+    # a custom mask (one window block dropped) keeps the token list
+    m2 = mask.clone()
+    m2[0, -2] = 0
+    assert decode_schedule(m2, n_q, n_kv, 1, 64, True, S, W).ring == 0
