@@ -16,9 +16,11 @@
 // Casts follow the reference: P^T -> dO dtype for dV, dS -> Q/K dtype for
 // dK/dQ, results stored in the input dtype.
 //
-// MI355X specifics: the KV-tile grid is ordered "heavy columns first" (the sink
-// column is kept by every q tile, so it runs longest); the remaining tiles are
-// XCD-remapped so neighbouring tiles of one head share L2.
+// MI355X specifics: the dK/dV grid runs a work list in which long column walks
+// (the sink column, kept by every q tile; the columns of a large grouped-query
+// group) are cut into items of bounded length whose fp32 partials a reduce
+// pass sums in a fixed order; items are XCD-remapped so neighbouring tiles of
+// one head share L2.
 #include "gki_common.cuh"
 
 namespace gki {
@@ -86,21 +88,60 @@ struct Stage32 {
   }
 };
 
-// Workgroup -> (bh, kv tile) for the dK/dV grid: the first n_heavy*BH blocks
-// take the heavy columns (spread round-robin over XCDs so they start first),
-// the rest walk each head's remaining columns in order, XCD-remapped.
-__device__ inline void dkdv_tile_of(int b, int BH, int n_kt, int n_heavy, const int32_t* order,
-                                    int& bh, int& kt) {
-  if (b < n_heavy * BH) {
-    bh = b % BH;
-    kt = order[b / BH];
-  } else {
-    const int n_rest = n_kt - n_heavy;
-    const int b2 = b - n_heavy * BH;
-    const int L = xcd_remap(b2, n_rest * BH);
-    bh = L / n_rest;
-    kt = order[n_heavy + (L - bh * n_rest)];
+// Work item of workgroup b in the dK / dV grid: the items of one (b, kv head)
+// are consecutive, XCD-remapped so that neighbouring kv tiles of a head (which
+// share most q tiles) run on one XCD and meet in its L2.
+struct KvItem {
+  int kt, it0, it1, pslot;
+};
+__device__ inline KvItem kv_item_of(int b, int BH, const KvWork& w, int& bh) {
+  const int wg = xcd_remap(b, w.n_items * BH);
+  bh = wg / w.n_items;
+  const int4 t = ((const int4*)w.items)[wg - bh * w.n_items];
+  return {t.x, t.y, t.z, t.w};
+}
+
+// Sum of a split column's fp32 partials, in item order, cast to the storage
+// type. A split column's 2 x 64 x D partial floats (dK then dV) are spread
+// over D / 8 workgroups, one float4 per thread; the loads of four partials are
+// issued together and added in item order (the sum is deterministic).
+template <int D>
+constexpr int kReduceWgPerTile = 2 * kTileN * D / (256 * 4);
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void dkdv_reduce_kernel(Geom g, KvWork w,
+                                                          typename T::storage* __restrict__ dK,
+                                                          typename T::storage* __restrict__ dV) {
+  constexpr int TILE = kTileN * D;                     // floats of one dK (or dV) tile
+  constexpr int STRIDE = 2 * TILE / 4;                 // float4s between two partials
+  constexpr int WGT = kReduceWgPerTile<D>;
+  const int rest = blockIdx.x / WGT, part = blockIdx.x - rest * WGT;
+  const int bh = rest / w.n_split, s = rest - bh * w.n_split;
+  const int kt = w.split[3 * s], p0 = w.split[3 * s + 1], np = w.split[3 * s + 2];
+  const int idx = (part * 256 + threadIdx.x) * 4;      // first float of this thread
+  const float4* src = (const float4*)(w.partials + ((size_t)bh * w.n_pslots + p0) * 2 * TILE + idx);
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  int c = 0;
+  for (; c + 4 <= np; c += 4) {
+    const float4 a0 = src[(size_t)c * STRIDE], a1 = src[(size_t)(c + 1) * STRIDE];
+    const float4 a2 = src[(size_t)(c + 2) * STRIDE], a3 = src[(size_t)(c + 3) * STRIDE];
+    acc.x = (((acc.x + a0.x) + a1.x) + a2.x) + a3.x;
+    acc.y = (((acc.y + a0.y) + a1.y) + a2.y) + a3.y;
+    acc.z = (((acc.z + a0.z) + a1.z) + a2.z) + a3.z;
+    acc.w = (((acc.w + a0.w) + a1.w) + a2.w) + a3.w;
   }
+  for (; c < np; ++c) {
+    const float4 a = src[(size_t)c * STRIDE];
+    acc.x += a.x, acc.y += a.y, acc.z += a.z, acc.w += a.w;
+  }
+  const int which = idx / TILE, rem = idx - which * TILE;   // 4 floats of one row (D % 4 == 0)
+  const int row = kt * kTileN + rem / D;
+  if (row >= g.n_kv) return;
+  typename T::storage* dst = (which ? dV : dK) + (size_t)bh * g.n_kv * D + (size_t)row * D + rem % D;
+  dst[0] = T::from_float(acc.x);
+  dst[1] = T::from_float(acc.y);
+  dst[2] = T::from_float(acc.z);
+  dst[3] = T::from_float(acc.w);
 }
 
 // ---------------------------------------------------------------------------
@@ -112,8 +153,7 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
     Geom g, const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const uint16_t* __restrict__ V, const uint16_t* __restrict__ dO, uint16_t* __restrict__ dK,
     uint16_t* __restrict__ dV, const float* __restrict__ LSE, const float* __restrict__ Delta,
-    const int32_t* __restrict__ col_ptr, const int32_t* __restrict__ col_idx,
-    const int32_t* __restrict__ order, int n_heavy, int n_kt) {
+    const int32_t* __restrict__ col_ptr, const int32_t* __restrict__ col_idx, KvWork w) {
   constexpr int KS = (D + 31) / 32;
   constexpr int DT = D / 16;
   using Tile = RowTile<D>;
@@ -122,11 +162,12 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
   __shared__ __align__(16) float slse[2][64];
   __shared__ __align__(16) float sdlt[2][64];
 
-  // one workgroup per (b, kv head, kv tile); with grouped-query attention it
-  // walks the CSC list once per q head of the group, accumulating in registers
+  // one workgroup per (b, kv head, work item): a range of the kv tile's walk
+  // over (q head of the group, CSC list entry), accumulated in registers
   const int BH = g.B * g.H_kv;
-  int bh, kt;
-  dkdv_tile_of(blockIdx.x, BH, n_kt, n_heavy, order, bh, kt);
+  int bh;
+  const KvItem item = kv_item_of(blockIdx.x, BH, w, bh);
+  const int kt = item.kt;
   const size_t kb = (size_t)bh * g.n_kv * D;
   const int bhq0 = (bh / g.H_kv) * g.H + (bh % g.H_kv) * g.group;   // first q head
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -172,10 +213,13 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
       dma_load4(src, lds_addr(wave_u == 0 ? slse[buf] : sdlt[buf]));
     }
   };
-  // iteration i visits list entry e of q head bhq; (e, bhq) advance together
-  const int n_it = (e_end - e_beg) * g.group;
-  int e_nx = e_beg, q_nx = bhq0;
-  if (n_it > 0) load_tile((col_idx[e_beg] & kIdxMask) * kTileM, bhq0, 0);
+  // iterations [it0, it1): iteration i visits list entry e_beg + i % L of q
+  // head bhq0 + i / L; (e, bhq) advance together
+  const int L = e_end - e_beg;
+  const int n_it = item.it1 - item.it0;
+  const int h0 = L > 0 ? item.it0 / L : 0;
+  int e_nx = e_beg + (item.it0 - h0 * L), q_nx = bhq0 + h0;
+  if (n_it > 0) load_tile((col_idx[e_nx] & kIdxMask) * kTileM, q_nx, 0);
   dma_wait();
   __syncthreads();
 
@@ -251,6 +295,20 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
   }
 
   // dK/dV accumulators: lane holds rows k_w + 4grp + i, column 16dt + col.
+  if (item.pslot >= 0) {             // a split column: fp32 partials for the reduce
+    float* pk = w.partials + ((size_t)bh * w.n_pslots + item.pslot) * 2 * (kTileN * D);
+    float* pv = pk + kTileN * D;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = wave * 16 + 4 * grp + i;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        pk[r * D + 16 * dt + col] = dk[dt][i];
+        pv[r * D + 16 * dt + col] = dv[dt][i];
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = k_w + 4 * grp + i;
@@ -280,18 +338,18 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_32(
     Geom g, const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ dO, float* __restrict__ dK, float* __restrict__ dV,
     const float* __restrict__ LSE, const float* __restrict__ Delta,
-    const int32_t* __restrict__ col_ptr, const int32_t* __restrict__ col_idx,
-    const int32_t* __restrict__ order, int n_heavy, int n_kt) {
+    const int32_t* __restrict__ col_ptr, const int32_t* __restrict__ col_idx, KvWork w) {
   constexpr int KS = D / 4;
   constexpr int DT = D / 16;
   constexpr int LD = D + 4;
   __shared__ __align__(16) DkdvSmem32<D> sm;
   Stage32<D> sq, sdo;
 
-  // one workgroup per (b, kv head, kv tile), looping over the group's q heads
+  // one workgroup per (b, kv head, work item), as in the 16-bit kernel
   const int BH = g.B * g.H_kv;
-  int bh, kt;
-  dkdv_tile_of(blockIdx.x, BH, n_kt, n_heavy, order, bh, kt);
+  int bh;
+  const KvItem item = kv_item_of(blockIdx.x, BH, w, bh);
+  const int kt = item.kt;
   const size_t kb = (size_t)bh * g.n_kv * D;
   const int bhq0 = (bh / g.H_kv) * g.H + (bh % g.H_kv) * g.group;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -322,9 +380,11 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_32(
       dreg = r < g.n_q ? Delta[(size_t)bhq * g.n_q + r] : 0.f;
     }
   };
-  const int n_it = (e_end - e_beg) * g.group;
-  int e_nx = e_beg, q_nx = bhq0;
-  if (n_it > 0) load_tile((col_idx[e_beg] & kIdxMask) * kTileM, bhq0);
+  const int L = e_end - e_beg;
+  const int n_it = item.it1 - item.it0;
+  const int h0 = L > 0 ? item.it0 / L : 0;
+  int e_nx = e_beg + (item.it0 - h0 * L), q_nx = bhq0 + h0;
+  if (n_it > 0) load_tile((col_idx[e_nx] & kIdxMask) * kTileM, q_nx);
 
   const int kv_hi_wave = min(k_w + 15, g.n_kv - 1);
   for (int it = 0; it < n_it; ++it) {
@@ -370,6 +430,20 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_32(
         }
       }
     }
+  }
+  if (item.pslot >= 0) {             // a split column: partials for the reduce
+    float* pk = w.partials + ((size_t)bh * w.n_pslots + item.pslot) * 2 * (kTileN * D);
+    float* pv = pk + kTileN * D;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = wave * 16 + 4 * grp + i;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        pk[r * D + 16 * dt + col] = dk[dt][i];
+        pv[r * D + 16 * dt + col] = dv[dt][i];
+      }
+    }
+    return;
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -634,15 +708,18 @@ template <int D>
 int launch_bwd(int dtype, const Geom& g, const void* q, const void* k, const void* v, const void* o,
                const void* dout, const float* lse, void* dq, void* dk, void* dv, float* delta,
                const int32_t* row_ptr, const int32_t* row_idx, int n_qt, const int32_t* col_ptr,
-               const int32_t* col_idx, const int32_t* order, int n_heavy, int n_kt,
-               hipStream_t stream) {
+               const int32_t* col_idx, const KvWork& w, hipStream_t stream) {
   const int BH = g.B * g.H, BHkv = g.B * g.H_kv;
   const int64_t rows = (int64_t)BH * g.n_q;
+  const dim3 kv_grid(w.n_items * BHkv), red_grid(w.n_split * BHkv * kReduceWgPerTile<D>);
   if (dtype == kF32) {
     launch_delta<F32, D>(o, dout, delta, rows, stream);
-    hipLaunchKernelGGL(dkdv_kernel_32<D>, dim3(n_kt * BHkv), dim3(256), 0, stream, g, (const float*)q,
+    hipLaunchKernelGGL(dkdv_kernel_32<D>, kv_grid, dim3(256), 0, stream, g, (const float*)q,
                        (const float*)k, (const float*)v, (const float*)dout, (float*)dk, (float*)dv,
-                       lse, delta, col_ptr, col_idx, order, n_heavy, n_kt);
+                       lse, delta, col_ptr, col_idx, w);
+    if (w.n_split > 0)
+      hipLaunchKernelGGL((dkdv_reduce_kernel<F32, D>), red_grid, dim3(256), 0, stream, g, w,
+                         (float*)dk, (float*)dv);
     hipLaunchKernelGGL(dq_kernel_32<D>, dim3(n_qt * BH), dim3(256), 0, stream, g, (const float*)q,
                        (const float*)k, (const float*)v, (const float*)dout, (float*)dq, lse, delta,
                        row_ptr, row_idx, n_qt);
@@ -652,20 +729,26 @@ int launch_bwd(int dtype, const Geom& g, const void* q, const void* k, const voi
                        (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
                        (const uint16_t*)o, (const uint16_t*)dout, (uint16_t*)dq, lse, delta,
                        row_ptr, row_idx, n_qt);
-    hipLaunchKernelGGL((dkdv_kernel_16<F16, D>), dim3(n_kt * BHkv), dim3(256), 0, stream, g,
+    hipLaunchKernelGGL((dkdv_kernel_16<F16, D>), kv_grid, dim3(256), 0, stream, g,
                        (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
                        (const uint16_t*)dout, (uint16_t*)dk, (uint16_t*)dv, lse, delta, col_ptr,
-                       col_idx, order, n_heavy, n_kt);
+                       col_idx, w);
+    if (w.n_split > 0)
+      hipLaunchKernelGGL((dkdv_reduce_kernel<F16, D>), red_grid, dim3(256), 0, stream, g, w,
+                         (uint16_t*)dk, (uint16_t*)dv);
   } else {
     // dQ first: it also produces Delta, which dK/dV reads
     hipLaunchKernelGGL((dq_kernel_16<BF16, D>), dim3(n_qt * BH), dim3(256), 0, stream, g,
                        (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
                        (const uint16_t*)o, (const uint16_t*)dout, (uint16_t*)dq, lse, delta,
                        row_ptr, row_idx, n_qt);
-    hipLaunchKernelGGL((dkdv_kernel_16<BF16, D>), dim3(n_kt * BHkv), dim3(256), 0, stream, g,
+    hipLaunchKernelGGL((dkdv_kernel_16<BF16, D>), kv_grid, dim3(256), 0, stream, g,
                        (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
                        (const uint16_t*)dout, (uint16_t*)dk, (uint16_t*)dv, lse, delta, col_ptr,
-                       col_idx, order, n_heavy, n_kt);
+                       col_idx, w);
+    if (w.n_split > 0)
+      hipLaunchKernelGGL((dkdv_reduce_kernel<BF16, D>), red_grid, dim3(256), 0, stream, g, w,
+                         (uint16_t*)dk, (uint16_t*)dv);
   }
   return check_launch("gki_bsa_bwd");
 }
@@ -675,12 +758,11 @@ int launch_bwd(int dtype, const Geom& g, const void* q, const void* k, const voi
 int bwd_dispatch(int dtype, int head_dim, const Geom& g, const void* q, const void* k, const void* v,
                  const void* o, const void* dout, const float* lse, void* dq, void* dk, void* dv,
                  float* delta, const int32_t* row_ptr, const int32_t* row_idx, int n_qt,
-                 const int32_t* col_ptr, const int32_t* col_idx, const int32_t* order, int n_heavy,
-                 int n_kt, hipStream_t stream) {
+                 const int32_t* col_ptr, const int32_t* col_idx, const KvWork& w, hipStream_t stream) {
 #define GKI_BWD_CASE(DD)                                                                          \
   case DD:                                                                                        \
     return launch_bwd<DD>(dtype, g, q, k, v, o, dout, lse, dq, dk, dv, delta, row_ptr, row_idx,   \
-                          n_qt, col_ptr, col_idx, order, n_heavy, n_kt, stream);
+                          n_qt, col_ptr, col_idx, w, stream);
   switch (head_dim) {
     GKI_BWD_CASE(16)
     GKI_BWD_CASE(32)

@@ -4,6 +4,8 @@
 // validates its arguments, launches, and returns 0 or a non-zero code whose
 // message is available from gki_last_error() (thread-local). The library never
 // allocates or frees device memory and keeps no pointer after returning.
+#include <algorithm>
+
 #include "gki_common.cuh"
 
 namespace gki {
@@ -32,8 +34,7 @@ int fwd_dispatch(int dtype, int head_dim, const Geom& g, const void* q, const vo
 int bwd_dispatch(int dtype, int head_dim, const Geom& g, const void* q, const void* k, const void* v,
                  const void* o, const void* dout, const float* lse, void* dq, void* dk, void* dv,
                  float* delta, const int32_t* row_ptr, const int32_t* row_idx, int n_qt,
-                 const int32_t* col_ptr, const int32_t* col_idx, const int32_t* order, int n_heavy,
-                 int n_kt, hipStream_t stream);
+                 const int32_t* col_ptr, const int32_t* col_idx, const KvWork& w, hipStream_t stream);
 int decode_tokens_dispatch(const Geom& g, const int32_t* list, int n_ent, int32_t* tok, int32_t* count,
                            hipStream_t stream);
 int decode_dispatch(int dtype, int head_dim, const Geom& g, const void* q, const void* k, const void* v,
@@ -99,7 +100,7 @@ using namespace gki;
 
 extern "C" {
 
-int gki_abi_version(void) { return 2; }
+int gki_abi_version(void) { return 3; }
 
 const char* gki_last_error(void) { return g_last_error.c_str(); }
 
@@ -134,7 +135,8 @@ int gki_bsa_bwd(const void* q, const void* k, const void* v, const void* o, cons
                 const float* lse, void* dq, void* dk, void* dv, float* delta, int32_t dtype, int32_t B,
                 int32_t H, int32_t H_kv, int32_t n_q, int32_t n_kv, int32_t head_dim, const int32_t* row_ptr,
                 const int32_t* row_idx, int32_t n_qt, const int32_t* col_ptr, const int32_t* col_idx,
-                const int32_t* kv_order, int32_t n_heavy, int32_t n_kt, const int32_t* mask,
+                int32_t n_kt, const int32_t* kv_items, int32_t n_items, const int32_t* kv_split,
+                int32_t n_split, int32_t n_pslots, float* kv_partials, const int32_t* mask,
                 int32_t n_qb, int32_t n_kb, int32_t block_m, int32_t block_n, float softmax_scale,
                 int32_t is_causal, int32_t sink_size, int32_t window_size, void* stream) {
   Geom g;
@@ -144,12 +146,70 @@ int gki_bsa_bwd(const void* q, const void* k, const void* v, const void* o, cons
   GKI_REQUIRE(q && k && v && o && dout && lse && dq && dk && dv && delta, 1, "gki_bsa_bwd: null tensor");
   GKI_REQUIRE(all_aligned16(q, k, v, o, dout, dq, dk, dv), 1,
               "gki_bsa_bwd: q, k, v, o, dout, dq, dk, dv must be 16-byte aligned");
-  GKI_REQUIRE(row_ptr && row_idx && col_ptr && col_idx && kv_order, 1, "gki_bsa_bwd: null schedule");
+  GKI_REQUIRE(row_ptr && row_idx && col_ptr && col_idx && kv_items, 1, "gki_bsa_bwd: null schedule");
   GKI_REQUIRE(n_qt == (n_q + kTileM - 1) / kTileM && n_kt == (n_kv + kTileN - 1) / kTileN, 1,
               "gki_bsa_bwd: schedule shape mismatch");
-  GKI_REQUIRE(n_heavy >= 0 && n_heavy <= n_kt, 1, "gki_bsa_bwd: bad heavy-column count");
+  GKI_REQUIRE(((uintptr_t)kv_items & 15) == 0, 1, "gki_bsa_bwd: kv_items must be 16-byte aligned");
+  GKI_REQUIRE(n_items >= n_kt && n_split >= 0 && n_pslots >= n_split && n_split <= n_kt, 1,
+              "gki_bsa_bwd: work list inconsistent with the tile count (see gki_dkdv_items)");
+  GKI_REQUIRE(n_split == 0 || (kv_split && kv_partials), 1,
+              "gki_bsa_bwd: split columns need kv_split and kv_partials");
+  GKI_REQUIRE((int64_t)n_items * B * H_kv < (1ll << 31) &&
+                  (int64_t)n_split * B * H_kv * (head_dim / 8) < (1ll << 31), 1,
+              "gki_bsa_bwd: dK/dV grid too large");
+  GKI_REQUIRE(((uintptr_t)kv_partials & 15) == 0, 1, "gki_bsa_bwd: kv_partials must be 16-byte aligned");
+  KvWork w{kv_items, n_items, kv_split, n_split, n_pslots, kv_partials};
   return bwd_dispatch(dtype, head_dim, g, q, k, v, o, dout, lse, dq, dk, dv, delta, row_ptr, row_idx,
-                      n_qt, col_ptr, col_idx, kv_order, n_heavy, n_kt, (hipStream_t)stream);
+                      n_qt, col_ptr, col_idx, w, (hipStream_t)stream);
+}
+
+int gki_dkdv_items(const int32_t* col_ptr, int32_t n_kt, int32_t group, int32_t bh_kv,
+                   int32_t* items, int32_t* n_items, int32_t* split, int32_t* n_split,
+                   int32_t* n_pslots) {
+  GKI_REQUIRE(col_ptr && n_items && n_split && n_pslots, 1, "gki_dkdv_items: null pointer");
+  GKI_REQUIRE(n_kt >= 1 && group >= 1 && bh_kv >= 1, 1,
+              "gki_dkdv_items: n_kt, group and bh_kv must be positive");
+  int64_t total = 0;
+  for (int kt = 0; kt < n_kt; ++kt) {
+    const int64_t len = (int64_t)col_ptr[kt + 1] - col_ptr[kt];
+    GKI_REQUIRE(len >= 0 && len * group < (1ll << 30), 1, "gki_dkdv_items: bad column list");
+    total += len;
+  }
+  total *= (int64_t)group * bh_kv;
+  // iterations per item: at least kDkdvMinChunk, and few enough that the whole
+  // grid has about kDkdvTargetItems items of work when columns are long
+  const int64_t chunk = std::max<int64_t>(kDkdvMinChunk, (total + kDkdvTargetItems - 1) / kDkdvTargetItems);
+  int32_t ni = 0, ns = 0, np = 0;
+  for (int kt = 0; kt < n_kt; ++kt) {
+    const int64_t n_it = ((int64_t)col_ptr[kt + 1] - col_ptr[kt]) * group;
+    const int64_t parts = std::max<int64_t>(1, (n_it + chunk - 1) / chunk);
+    if (parts == 1) {
+      if (items) {
+        int32_t* it = items + 4 * ni;
+        it[0] = kt, it[1] = 0, it[2] = (int32_t)n_it, it[3] = -1;
+      }
+      ++ni;
+      continue;
+    }
+    if (split) {
+      int32_t* sp = split + 3 * ns;
+      sp[0] = kt, sp[1] = np, sp[2] = (int32_t)parts;
+    }
+    ++ns;
+    for (int64_t c = 0; c < parts; ++c) {
+      if (items) {
+        int32_t* it = items + 4 * ni;
+        it[0] = kt, it[1] = (int32_t)(n_it * c / parts), it[2] = (int32_t)(n_it * (c + 1) / parts);
+        it[3] = np + (int32_t)c;
+      }
+      ++ni;
+    }
+    np += (int32_t)parts;
+  }
+  *n_items = ni;
+  *n_split = ns;
+  *n_pslots = np;
+  return 0;
 }
 
 int64_t gki_bsa_decode_workspace_floats(int32_t B, int32_t H, int32_t n_q, int32_t head_dim,

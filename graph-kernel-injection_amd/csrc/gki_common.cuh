@@ -271,6 +271,10 @@ constexpr int kTileN = 64;       // kv rows of every tile
 constexpr int kTileMF = 128;     // q rows of the forward tile (4 waves x 32 rows)
 constexpr int kDecodeTileM = 16;
 constexpr int kDecodeMaxQ = 4;
+// dK/dV work items: at least kDkdvMinChunk iterations each, and about
+// kDkdvTargetItems items over the whole grid when the column walks are long.
+constexpr int kDkdvMinChunk = 32;
+constexpr int kDkdvTargetItems = 8192;
 
 // q heads one decode workgroup serves: a whole group of grouped-query heads
 // when its group * n_q rows fit the kernel's row limit (K / V read once per
@@ -302,6 +306,22 @@ struct Geom {
   // original block mask (used only for tiles flagged partial)
   const int32_t* mask;
   int n_qb, n_kb, bm, bn;
+};
+
+// Work list of the dK / dV grid (built on the host by gki_dkdv_items). A kv
+// tile's walk -- group x (its kept q tiles) iterations, iteration i visiting
+// list entry i % L of q head i / L -- is cut into items of at most a chunk of
+// iterations, so no workgroup carries a long column (the sink column, the
+// columns of a large grouped-query group) alone. A column with one item stores
+// dK / dV itself; the items of a split column store fp32 partials, which a
+// reduce pass sums in item order (deterministic).
+struct KvWork {
+  const int32_t* items;   // [n_items][4]: kv tile, first iteration, end iteration, partial slot (-1: none)
+  int n_items;
+  const int32_t* split;   // [n_split][3]: kv tile, its first partial slot, number of slots
+  int n_split;
+  int n_pslots;           // partial slots per (b, kv head)
+  float* partials;        // [B * H_kv][n_pslots][2 (dK, dV)][64][D] fp32
 };
 
 // (b, q head) -> (b, kv head) row index of K / V (and dK / dV).

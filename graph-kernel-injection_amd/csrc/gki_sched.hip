@@ -14,8 +14,6 @@
 // * The list kernels turn a {0,1,2} matrix into CSR (rows -> ascending columns)
 //   and CSC (columns -> ascending rows) int32 lists, entry = index | (v==2)<<30.
 //   Applied to a 0/1 block mask they give exactly `mask.nonzero()` order.
-// * heavy_order_kernel lists "heavy" columns (kept by far more rows than the
-//   mean, e.g. the StreamingLLM sink column) first for the dK/dV grid.
 #include "gki_common.cuh"
 
 namespace gki {
@@ -156,49 +154,6 @@ __global__ __launch_bounds__(256) void fill_kernel(const int32_t* __restrict__ m
   }
 }
 
-// Heavy columns first (ascending index), then the rest (ascending index).
-__global__ __launch_bounds__(1024) void heavy_order_kernel(const int32_t* __restrict__ col_ptr,
-                                                           int n_cols, int32_t* __restrict__ order,
-                                                           int32_t* __restrict__ n_heavy_out) {
-  __shared__ int wsum[16];
-  __shared__ int carry[2];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const long long total = col_ptr[n_cols];
-  // heavy: kept by more than twice the mean number of rows (and at least 4)
-  auto is_heavy = [&](int j) {
-    const long long c = col_ptr[j + 1] - col_ptr[j];
-    return c >= 4 && c * (long long)n_cols > 2 * total;
-  };
-  for (int pass = 0; pass < 2; ++pass) {
-    if (threadIdx.x == 0) carry[0] = 0;
-    __syncthreads();
-    const int heavy_total = pass == 1 ? carry[1] : 0;
-    for (int base = 0; base < n_cols; base += 1024) {
-      const int j = base + threadIdx.x;
-      const bool sel = j < n_cols && (pass == 0 ? is_heavy(j) : !is_heavy(j));
-      const unsigned long long bal = __ballot(sel);
-      const int below = __popcll(bal & ((1ull << lane) - 1ull));
-      if (lane == 0) wsum[wave] = __popcll(bal);
-      __syncthreads();
-      int off = carry[0];
-      for (int w = 0; w < wave; ++w) off += wsum[w];
-      if (sel) order[heavy_total + off + below] = j;
-      __syncthreads();
-      if (threadIdx.x == 0) {
-        int s = 0;
-        for (int w = 0; w < 16; ++w) s += wsum[w];
-        carry[0] += s;
-      }
-      __syncthreads();
-    }
-    if (pass == 0 && threadIdx.x == 0) {
-      carry[1] = carry[0];
-      *n_heavy_out = carry[0];
-    }
-    __syncthreads();
-  }
-}
-
 inline unsigned blocks_for(int64_t n, int bs) { return (unsigned)((n + bs - 1) / bs); }
 
 }  // namespace
@@ -275,15 +230,6 @@ int gki_block_list_fill(const int32_t* m, int32_t n_rows, int32_t n_cols, const 
     hipLaunchKernelGGL(fill_kernel<true>, dim3(n_cols), dim3(256), 0, s, m, n_rows, n_cols, col_ptr,
                        col_idx);
   return check_launch("gki_block_list_fill");
-}
-
-int gki_heavy_order(const int32_t* col_ptr, int32_t n_cols, int32_t* order, int32_t* n_heavy,
-                    void* stream) {
-  GKI_REQUIRE(col_ptr && order && n_heavy, 1, "gki_heavy_order: null pointer");
-  GKI_REQUIRE(n_cols > 0, 1, "gki_heavy_order: n_cols must be positive");
-  hipLaunchKernelGGL(heavy_order_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, col_ptr, n_cols,
-                     order, n_heavy);
-  return check_launch("gki_heavy_order");
 }
 
 }  // extern "C"

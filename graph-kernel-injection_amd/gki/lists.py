@@ -12,7 +12,8 @@ mask is turned once, on the GPU, into int32 lists:
   fp32; backward 64x64; decode 16x64). A mask of any block size is first
   classified per tile by ``gki_tile_mask`` (token-rule aware when causal, so
   tiles with nothing visible are not visited). The backward schedule adds the
-  "heavy columns first" order for the dK/dV grid; the decode schedule adds the
+  dK/dV work list (``gki_dkdv_items``: long kv-tile walks cut into near-equal
+  items whose fp32 partials are summed in order); the decode schedule adds the
   token-exact stream of visible positions.
 
 Schedules are cached per mask tensor (identity, version, geometry) and shared
@@ -57,8 +58,11 @@ class FwdSchedule:
 @dataclass(frozen=True)
 class BwdSchedule:
     lists: BlockLists         # over 64x64 tiles (n_qt x n_kt)
-    kv_order: torch.Tensor    # [n_kt] int32, heavy columns first
-    n_heavy: int
+    items: torch.Tensor       # [n_items, 4] int32 (kv tile, first it, end it, slot | -1)
+    n_items: int
+    split: torch.Tensor       # [max(n_split, 1), 3] int32 (kv tile, first slot, slots)
+    n_split: int
+    n_pslots: int             # fp32 partial slots per (b, kv head)
     n_qt: int
     n_kt: int
 
@@ -204,23 +208,43 @@ def fwd_schedule(mask: torch.Tensor, n_q: int, n_kv: int, block_m: int, block_n:
     return _CACHE.get(mask, key, build)
 
 
+def dkdv_items(col_ptr_host: torch.Tensor, group: int, bh_kv: int):
+    """The dK/dV work list of CSC column pointers (a host int32 tensor):
+    (items [n_items, 4], split [max(n_split, 1), 3], n_items, n_split, n_pslots),
+    host int32 tensors, from ``gki_dkdv_items``."""
+    lib = _lib.load()
+    ptr = col_ptr_host.to(torch.int32).contiguous()
+    n_kt = ptr.numel() - 1
+    counts = [ctypes.c_int32() for _ in range(3)]
+    refs = [ctypes.addressof(c) for c in counts]
+    _lib.check(lib.gki_dkdv_items(ptr.data_ptr(), n_kt, group, bh_kv, None, refs[0], None, refs[1],
+                                  refs[2]), "gki_dkdv_items")
+    n_items, n_split, _ = (c.value for c in counts)
+    items = torch.empty((n_items, 4), dtype=torch.int32)
+    split = torch.zeros((max(n_split, 1), 3), dtype=torch.int32)
+    _lib.check(lib.gki_dkdv_items(ptr.data_ptr(), n_kt, group, bh_kv, items.data_ptr(), refs[0],
+                                  split.data_ptr(), refs[1], refs[2]), "gki_dkdv_items")
+    return items, split, counts[0].value, counts[1].value, counts[2].value
+
+
 def bwd_schedule(mask: torch.Tensor, n_q: int, n_kv: int, block_m: int, block_n: int,
-                 is_causal: bool, sink: int, window: int) -> BwdSchedule:
-    """CSR + CSC schedules of the dQ and dK/dV kernels (64x64 tiles)."""
+                 is_causal: bool, sink: int, window: int, group: int = 1,
+                 bh_kv: int = 1) -> BwdSchedule:
+    """CSR + CSC schedules of the dQ and dK/dV kernels (64x64 tiles) and the
+    dK/dV work list for ``group`` q heads per kv head over ``bh_kv`` = B * H_kv
+    (b, kv head) pairs."""
     ts = _lib.tile_sizes()
     tm, tn = ts["bwd_tile_m"], ts["tile_n"]
 
     def build() -> BwdSchedule:
-        lib = _lib.load()
         tiles = tile_matrix(mask, n_q, n_kv, block_m, block_n, tm, tn, is_causal, sink, window)
         lists = _lists_of(tiles)
-        order = torch.empty(lists.n_cols, dtype=torch.int32, device=mask.device)
-        n_heavy = torch.empty(1, dtype=torch.int32, device=mask.device)
-        _lib.check(lib.gki_heavy_order(lists.col_ptr.data_ptr(), lists.n_cols, order.data_ptr(),
-                                       n_heavy.data_ptr(), _stream(mask.device)), "gki_heavy_order")
-        return BwdSchedule(lists, order, int(n_heavy.item()), lists.n_rows, lists.n_cols)
+        items, split, n_items, n_split, n_pslots = dkdv_items(lists.col_ptr.cpu(), group, bh_kv)
+        dev = mask.device
+        return BwdSchedule(lists, items.to(dev), n_items, split.to(dev), n_split, n_pslots,
+                           lists.n_rows, lists.n_cols)
 
-    key = ("bwd", n_q, n_kv, block_m, block_n, tm, tn, bool(is_causal), sink, window)
+    key = ("bwd", n_q, n_kv, block_m, block_n, tm, tn, bool(is_causal), sink, window, group, bh_kv)
     return _CACHE.get(mask, key, build)
 
 

@@ -190,14 +190,19 @@ class _BlockSparseFlashAttention(torch.autograd.Function):
         with torch.cuda.device(q.device):
             stream = torch.cuda.current_stream(q.device).cuda_stream
             sched = bwd_schedule(block_mask, N_Q, N_KV, ctx.block_m, ctx.block_n, ctx.is_causal,
-                                 ctx.sink_size, ctx.window_size)
+                                 ctx.sink_size, ctx.window_size, group=H // H_kv, bh_kv=B * H_kv)
             L = sched.lists
+            # fp32 dK / dV partials of the split kv tiles: [B*H_kv, n_pslots, 2, 64, D]
+            tile_n = _lib.tile_sizes()["tile_n"]
+            partials = torch.empty(max(B * H_kv * sched.n_pslots * 2 * tile_n * D, 1),
+                                   dtype=torch.float32, device=q.device)
             _lib.check(lib.gki_bsa_bwd(
                 q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(),
                 lse.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), delta.data_ptr(),
                 _DTYPE_CODE[q.dtype], B, H, H_kv, N_Q, N_KV, D, L.row_ptr.data_ptr(),
                 L.row_idx.data_ptr(), sched.n_qt, L.col_ptr.data_ptr(), L.col_idx.data_ptr(),
-                sched.kv_order.data_ptr(), sched.n_heavy, sched.n_kt, block_mask.data_ptr(), n_qb,
+                sched.n_kt, sched.items.data_ptr(), sched.n_items, sched.split.data_ptr(),
+                sched.n_split, sched.n_pslots, partials.data_ptr(), block_mask.data_ptr(), n_qb,
                 n_kb, ctx.block_m, ctx.block_n, float(ctx.softmax_scale), int(ctx.is_causal),
                 ctx.sink_size, ctx.window_size, stream), "gki_bsa_bwd")
         return (dq, dk, dv) + (None,) * (7 + ctx.n_extra)

@@ -34,7 +34,8 @@
 extern "C" {
 #endif
 
-/* ABI version (currently 2: grouped-query attention, H_kv after H). */
+/* ABI version (currently 3: grouped-query attention, H_kv after H; dK/dV work
+ * items from gki_dkdv_items). */
 int gki_abi_version(void);
 
 /* Message of the last failing call on this thread. */
@@ -86,11 +87,20 @@ int gki_block_list_fill(const int32_t* m, int32_t n_rows, int32_t n_cols,
                         const int32_t* row_ptr, const int32_t* col_ptr,
                         int32_t* row_idx, int32_t* col_idx, void* stream);
 
-/* Column order for the dK/dV grid: columns kept by more than twice the mean
- * row count (the StreamingLLM sink column) first, then the rest, each group
- * ascending. Writes n_cols indices and the heavy count (device scalar). */
-int gki_heavy_order(const int32_t* col_ptr, int32_t n_cols, int32_t* order,
-                    int32_t* n_heavy, void* stream);
+/* Work list of the dK/dV grid (host arrays; no reference counterpart -- the
+ * reference runs one program per kv tile, sparse_triton_kernel.py:719-777).
+ * col_ptr: the CSC column pointers (n_kt + 1, host copy) of the backward tiles;
+ * group: q heads per K/V head; bh_kv: B * H_kv. A kv tile's walk of
+ * group x (its list length) iterations becomes one item, or -- when longer than
+ * the chunk max(32, ceil(total iterations / 8192)) -- several near-equal items
+ * whose fp32 partials gki_bsa_bwd sums in item order (deterministic). Writes
+ * items [n_items][4] = (kv tile, first iteration, end iteration, partial slot or
+ * -1) and split [n_split][3] = (kv tile, first slot, slot count), and the counts;
+ * pass items = split = NULL to size them first. n_pslots partial slots per
+ * (b, kv head) need 2 * 64 * head_dim floats each. */
+int gki_dkdv_items(const int32_t* col_ptr, int32_t n_kt, int32_t group, int32_t bh_kv,
+                   int32_t* items, int32_t* n_items, int32_t* split, int32_t* n_split,
+                   int32_t* n_pslots);
 
 /* Prefill forward: replaces the `_fwd_kernel` launch in
  * `_BlockSparseFlashAttention.forward` (sparse_triton_kernel.py:662-682).
@@ -106,8 +116,10 @@ int gki_bsa_fwd(const void* q, const void* k, const void* v, void* o, float* lse
 
 /* Backward: replaces the three launches in `_BlockSparseFlashAttention.backward`
  * (sparse_triton_kernel.py:719-777): the row terms Delta = rowsum(O * dO), dK/dV
- * over the CSC list (kv_order / n_heavy from gki_heavy_order) and dQ over the
- * CSR list, both over bwd_tile_m x tile_n tiles. `delta` is a caller-owned fp32
+ * over the CSC list (device copies of gki_dkdv_items' lists: kv_items 16-byte
+ * aligned; kv_partials a 16-byte aligned fp32 workspace
+ * [B * H_kv][n_pslots][2][64][head_dim], needed when n_split > 0) and dQ over
+ * the CSR list, both over bwd_tile_m x tile_n tiles. `delta` is a caller-owned fp32
  * [B, H, N_Q] workspace for the row terms (its contents on return are internal:
  * Delta for fp32 inputs, Delta * softmax_scale for fp16 / bf16). dq, dk, dv are
  * fully written (no zero-fill needed). */
@@ -116,8 +128,10 @@ int gki_bsa_bwd(const void* q, const void* k, const void* v, const void* o,
                 float* delta, int32_t dtype, int32_t B, int32_t H, int32_t H_kv,
                 int32_t n_q, int32_t n_kv, int32_t head_dim, const int32_t* row_ptr,
                 const int32_t* row_idx, int32_t n_qt, const int32_t* col_ptr,
-                const int32_t* col_idx, const int32_t* kv_order, int32_t n_heavy,
-                int32_t n_kt, const int32_t* mask, int32_t n_qb, int32_t n_kb,
+                const int32_t* col_idx, int32_t n_kt, const int32_t* kv_items,
+                int32_t n_items, const int32_t* kv_split, int32_t n_split,
+                int32_t n_pslots, float* kv_partials, const int32_t* mask,
+                int32_t n_qb, int32_t n_kb,
                 int32_t block_m, int32_t block_n, float softmax_scale, int32_t is_causal,
                 int32_t sink_size, int32_t window_size, void* stream);
 

@@ -17,6 +17,10 @@ How each is pinned (by the tests in ``tests/test_oracle_pins.py``):
   restated) on the reference's 13 shapes.
 * ``dense_block_mask``    -- sparse_triton_kernel.py:184-210. Pinned by brute force.
 * ``kept_lists``          -- build-only (CSR/CSC). Pinned by ``np.nonzero``.
+* ``dkdv_items``          -- build-only dK/dV work list. Pinned by its
+  invariants: every kv tile's iterations covered once, in order, by items of
+  at most ``chunk`` iterations whose lengths differ by at most one; slots
+  numbered consecutively per split tile; the unsplit case one item per tile.
 * ``tile_classes``        -- build-only tile classification. Pinned per tile
   against ``effective_mask`` (visited iff some effective element; class 1 iff
   the effective mask equals the token rule there).
@@ -141,14 +145,33 @@ def tile_classes(mask: np.ndarray, n_q: int, n_kv: int, bm: int, bn: int, tm: in
     return out
 
 
-def heavy_order(col_ptr: np.ndarray) -> Tuple[np.ndarray, int]:
-    """Columns kept by > 2x the mean rows (and >= 4) first, then the rest."""
+def dkdv_items(col_ptr: np.ndarray, group: int, bh_kv: int, chunk: Optional[int] = None,
+               min_chunk: int = 32, target_items: int = 8192):
+    """The dK/dV work list (build-only; the reference runs one program per kv
+    tile, sparse_triton_kernel.py:719-777). A kv tile's walk of group x (its
+    column length) iterations is one item (slot -1) when it fits the chunk,
+    else ``parts = ceil(n_it / chunk)`` items ``[n_it*c/parts, n_it*(c+1)/parts)``
+    writing consecutive partial slots. ``chunk`` defaults to
+    ``max(min_chunk, ceil(total / target_items))`` with
+    ``total = sum(len) * group * bh_kv``. Returns (items [n, 4], split [m, 3],
+    n_pslots) as int32 arrays: items (kv tile, first, end, slot | -1), split
+    (kv tile, first slot, slot count)."""
     cnt = np.diff(col_ptr.astype(np.int64))
-    n = len(cnt)
-    total = int(cnt.sum())
-    heavy = (cnt >= 4) & (cnt * n > 2 * total)
-    order = np.concatenate([np.nonzero(heavy)[0], np.nonzero(~heavy)[0]]).astype(np.int32)
-    return order, int(heavy.sum())
+    if chunk is None:
+        total = int(cnt.sum()) * group * bh_kv
+        chunk = max(min_chunk, -(-total // target_items))
+    items, split, n_pslots = [], [], 0
+    for kt, n in enumerate(cnt):
+        n_it = int(n) * group
+        parts = max(1, -(-n_it // chunk))
+        if parts == 1:
+            items.append((kt, 0, n_it, -1))
+            continue
+        split.append((kt, n_pslots, parts))
+        items += [(kt, n_it * c // parts, n_it * (c + 1) // parts, n_pslots + c) for c in range(parts)]
+        n_pslots += parts
+    return (np.array(items, np.int32).reshape(-1, 4), np.array(split, np.int32).reshape(-1, 3),
+            n_pslots)
 
 
 # ---------------------------------------------------------------------------

@@ -106,17 +106,18 @@ def test_schedules_match_oracle(n_q, n_kv, sink, window, bm, bn, causal):
     m = so.block_mask(n_q, n_kv, sink, window, bm, bn)
     dm = torch.from_numpy(m).to(DEV)
     ts = _lib.tile_sizes()
-    # backward: CSR + CSC over 64x64 tiles, heavy-first column order
-    sched = bwd_schedule(dm, n_q, n_kv, bm, bn, causal, sink, window)
+    # backward: CSR + CSC over 64x64 tiles and the dK/dV work list
+    sched = bwd_schedule(dm, n_q, n_kv, bm, bn, causal, sink, window, group=2, bh_kv=3)
     tiles = so.tile_classes(m, n_q, n_kv, bm, bn, ts["bwd_tile_m"], ts["tile_n"], causal, sink,
                             window)
     ref = so.kept_lists(tiles)
     L = sched.lists
     for got, want in zip((L.row_ptr, L.row_idx, L.col_ptr, L.col_idx), ref):
         np.testing.assert_array_equal(got.cpu().numpy(), want)
-    order, n_heavy = so.heavy_order(ref[2])
-    np.testing.assert_array_equal(sched.kv_order.cpu().numpy(), order)
-    assert sched.n_heavy == n_heavy
+    items, split, n_pslots = so.dkdv_items(ref[2], 2, 3)
+    np.testing.assert_array_equal(sched.items.cpu().numpy(), items)
+    np.testing.assert_array_equal(sched.split.cpu().numpy()[:sched.n_split], split)
+    assert (sched.n_items, sched.n_split, sched.n_pslots) == (len(items), len(split), n_pslots)
     # forward: CSR over the per-dtype q tiles
     for fp32, key in ((False, "fwd_tile_m_16"), (True, "fwd_tile_m_32")):
         fs = fwd_schedule(dm, n_q, n_kv, bm, bn, causal, sink, window, fp32)
@@ -325,6 +326,54 @@ def _forward_lse(q, k, v, mask, bm, bn, S, W):
     out = stk.block_sparse_attention(*leaves, mask, block_m=bm, block_n=bn, is_causal=True,
                                      sink_size=S, window_size=W)
     return out.grad_fn.saved_tensors[4]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("chunk", [1, 5, 1 << 20])
+def test_dkdv_any_cut_of_the_work_list_matches_oracle(chunk, dtype):
+    """gki_bsa_bwd through the C ABI with the dK/dV work list cut at any chunk
+    (1 iteration per item, 5, never): every cut gives the oracle's gradients,
+    grouped-query (4 q heads per kv head) so items also split inside a group.
+    Inputs N(0, 0.5) as the configs': at N(0, 1) the uncut fp32 walk of the sink
+    keys (44 iterations, sum of P 30 to 40) reaches 1.08e-5 of dV against the
+    1e-5 bar, the fp32 rounding of the saved LSE carried by every P."""
+    B, H_kv, group, N, D, S, W, bm = 1, 2, 4, 700, 64, 4, 128, 64
+    H = H_kv * group
+    print(f"[case] work list chunk {chunk} {dtype}", flush=True)
+    q, k, v, do = _inputs((B, H, N, D), (B, H_kv, N, D), dtype, seed=31, scale=0.5, grad_out=True)
+    mask = stk.make_streaming_mask(N, N, stk.StreamingMaskSpec(S, W), bm, bm, device=DEV)
+    leaves = [t.detach().requires_grad_(True) for t in (q, k, v)]
+    out = stk.block_sparse_attention(*leaves, mask, block_m=bm, block_n=bm, is_causal=True,
+                                     sink_size=S, window_size=W, enable_gqa=True)
+    lse = out.grad_fn.saved_tensors[4]
+    sched = bwd_schedule(mask, N, N, bm, bm, True, S, W, group=group, bh_kv=B * H_kv)
+    L = sched.lists
+    items, split, n_pslots = so.dkdv_items(L.col_ptr.cpu().numpy(), group, B * H_kv, chunk=chunk)
+    assert (len(split) > 0) == (chunk < 1 << 20)
+    items_d = torch.from_numpy(items).to(DEV)
+    split_d = torch.from_numpy(split if len(split) else np.zeros((1, 3), np.int32)).to(DEV)
+    partials = torch.empty(max(B * H_kv * n_pslots * 2 * 64 * D, 1), dtype=torch.float32, device=DEV)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    delta = torch.empty((B, H, N), dtype=torch.float32, device=DEV)
+    code = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}[dtype]
+    n_b = (N + bm - 1) // bm
+    lib = _lib.load()
+    rc = lib.gki_bsa_bwd(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), do.data_ptr(), lse.data_ptr(),
+        dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), delta.data_ptr(), code, B, H, H_kv, N, N, D,
+        L.row_ptr.data_ptr(), L.row_idx.data_ptr(), sched.n_qt, L.col_ptr.data_ptr(),
+        L.col_idx.data_ptr(), sched.n_kt, items_d.data_ptr(), len(items), split_d.data_ptr(),
+        len(split), n_pslots, partials.data_ptr(), mask.data_ptr(), n_b, n_b, bm, bm,
+        1.0 / math.sqrt(D), 1, S, W, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, lib.gki_last_error()
+    torch.cuda.synchronize()
+    eff = so.effective_mask(mask.cpu().numpy(), N, N, bm, bm, True, S, W)
+    qn, kn, vn, don = (t.to(torch.float64).cpu().numpy() for t in (q, k, v, do))
+    grads = so.attention_bwd(qn, so.expand_kv_heads(kn, group), so.expand_kv_heads(vn, group), don,
+                             eff, 1.0 / math.sqrt(D))
+    _close(dq, torch.from_numpy(grads[0]), dtype, f"dQ chunk {chunk}")
+    _close(dk, torch.from_numpy(so.reduce_kv_grad(grads[1], group)), dtype, f"dK chunk {chunk}")
+    _close(dv, torch.from_numpy(so.reduce_kv_grad(grads[2], group)), dtype, f"dV chunk {chunk}")
 
 
 def test_config3_train_fp16_full():

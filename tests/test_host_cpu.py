@@ -94,7 +94,42 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(lib, name), f"{name} declared in gki_bsa.h but not exported"
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
     assert set(_lib.SIGNATURES) == set(names)
-    assert lib.gki_abi_version() == 2
+    assert lib.gki_abi_version() == 3
+
+
+def test_dkdv_work_list_matches_oracle():
+    """gki_dkdv_items (host code) equals the oracle's plan bit for bit, including
+    empty columns, a single tile and sizes that split many columns."""
+    from gki.lists import dkdv_items
+
+    rng = np.random.default_rng(9)
+    cases = [(np.array([0, 0]), 1, 1), (np.array([0, 5]), 4, 1)]
+    for _ in range(40):
+        n_kt = int(rng.integers(1, 300))
+        cnt = rng.integers(0, 200, n_kt)
+        cnt[rng.random(n_kt) < 0.1] = 0
+        cases.append((np.concatenate([[0], np.cumsum(cnt)]), int(rng.choice([1, 2, 4, 8])),
+                      int(rng.integers(1, 128))))
+    m = so.block_mask(131072, 131072, 4, 4096, 64, 64)
+    cases.append((so.kept_lists(m)[2], 1, 16))
+    for col_ptr, group, bh_kv in cases:
+        col_ptr = col_ptr.astype(np.int32)
+        items, split, n_items, n_split, n_pslots = dkdv_items(torch.from_numpy(col_ptr), group, bh_kv)
+        want_items, want_split, want_np = so.dkdv_items(col_ptr, group, bh_kv)
+        np.testing.assert_array_equal(items.numpy(), want_items)
+        assert n_items == len(want_items) and n_split == len(want_split) and n_pslots == want_np
+        np.testing.assert_array_equal(split.numpy()[:n_split], want_split)
+
+
+def test_dkdv_work_list_rejects_bad_columns():
+    lib = _lib.load()
+    out = [ctypes.c_int32() for _ in range(3)]
+    refs = [ctypes.addressof(c) for c in out]
+    bad = np.array([0, 5, 3], np.int32)                         # decreasing pointer
+    assert lib.gki_dkdv_items(bad.ctypes.data, 2, 1, 1, None, refs[0], None, refs[1], refs[2]) == 1
+    assert b"column" in lib.gki_last_error()
+    ok = np.array([0, 5], np.int32)
+    assert lib.gki_dkdv_items(ok.ctypes.data, 1, 0, 1, None, refs[0], None, refs[1], refs[2]) == 1
 
 
 def test_tile_sizes():

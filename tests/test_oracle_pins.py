@@ -204,12 +204,57 @@ def test_tile_classes_causal_against_effective_mask(n_q, n_kv, sink, window, bm,
             assert not (t == 2).any()
 
 
-def test_heavy_order_puts_sink_column_first():
-    m = so.block_mask(8192, 8192, 4, 1024, 64, 64)
+def _check_work_list(col_ptr, group, items, split, n_pslots, chunk):
+    """Invariants of a dK/dV work list over CSC column pointers."""
+    cnt = np.diff(col_ptr.astype(np.int64)) * group
+    assert items.shape[1] == 4 and split.shape[1] == 3
+    assert sorted(set(items[:, 0].tolist())) == list(range(len(cnt)))
+    assert (np.diff(items[:, 0]) >= 0).all()               # tiles in order
+    splits = {int(kt): (int(p0), int(n)) for kt, p0, n in split}
+    next_slot = 0
+    for kt, n_it in enumerate(cnt):
+        it = items[items[:, 0] == kt]
+        assert it[0, 1] == 0 and it[-1, 2] == n_it         # covers [0, n_it)
+        assert (it[1:, 1] == it[:-1, 2]).all()             # contiguous, no overlap
+        lens = it[:, 2] - it[:, 1]
+        if len(it) == 1:
+            assert it[0, 3] == -1 and kt not in splits and n_it <= chunk
+            continue
+        assert lens.max() <= chunk and lens.max() - lens.min() <= 1
+        assert len(it) == -(-n_it // chunk)
+        p0, n = splits[kt]
+        assert p0 == next_slot and n == len(it)
+        assert it[:, 3].tolist() == list(range(p0, p0 + n))
+        next_slot += n
+    assert n_pslots == next_slot
+
+
+def test_dkdv_work_list_invariants():
+    rng = np.random.default_rng(5)
+    for _ in range(60):
+        n_kt = int(rng.integers(1, 40))
+        cnt = rng.integers(0, 90, n_kt)
+        cnt[rng.random(n_kt) < 0.2] = 0
+        col_ptr = np.concatenate([[0], np.cumsum(cnt)]).astype(np.int32)
+        group, bh_kv = int(rng.choice([1, 2, 4, 8])), int(rng.integers(1, 64))
+        for chunk in (None, 1, int(rng.integers(2, 50))):
+            items, split, n_pslots = so.dkdv_items(col_ptr, group, bh_kv, chunk=chunk)
+            c = chunk or max(32, -(-int(cnt.sum()) * group * bh_kv // 8192))
+            _check_work_list(col_ptr, group, items, split, n_pslots, c)
+
+
+def test_dkdv_work_list_splits_only_long_columns():
+    """Config 5's mask (S 4, W 4096, 64x64 tiles, N 131072): the sink column
+    (all 2048 q tiles) is cut; window columns (<= 65 q tiles) are not. A huge
+    chunk gives one item per tile and no split."""
+    m = so.block_mask(131072, 131072, 4, 4096, 64, 64)
     _, _, col_ptr, _ = so.kept_lists(m)
-    order, n_heavy = so.heavy_order(col_ptr)
-    assert n_heavy == 1 and order[0] == 0
-    assert sorted(order.tolist()) == list(range(128))
+    items, split, n_pslots = so.dkdv_items(col_ptr, 1, 16)
+    assert split[:, 0].tolist() == [0]
+    assert split[0, 2] == n_pslots == -(-2048 // max(32, -(-int(col_ptr[-1]) * 16 // 8192)))
+    items, split, n_pslots = so.dkdv_items(col_ptr, 1, 16, chunk=1 << 20)
+    assert len(items) == len(col_ptr) - 1 and len(split) == 0 and n_pslots == 0
+    assert (items[:, 3] == -1).all()
 
 
 # ---------------------------------------------------------------------------
