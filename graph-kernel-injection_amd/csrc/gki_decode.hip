@@ -268,7 +268,10 @@ __device__ inline void decode_consume(const Geom& g, const DecodeRound<T, D, NU>
 // slots for a rolling one). A workgroup serves gq consecutive q heads of one kv
 // head (gq = group when group * n_q <= kDecodeMaxQ, else 1): its n_rows =
 // gq * n_q rows are rows bhq0 * n_q + r of Q / O / LSE, r = head * n_q + query
-// row, and share every K / V load.
+// row, and share every K / V load. Workgroups run in the logical order (kv
+// stream, split, q head of the stream's group), XCD-remapped: when the q heads
+// of a group get one workgroup each (gq = 1), those reading one K / V slice are
+// neighbours on one XCD and share its L2 (one HBM read per slice, not group).
 template <typename T, int D, int NQ, typename Src, bool EXACT>
 __global__ __launch_bounds__(64 * decode_waves<NQ>()) void decode_kernel(
     Geom g, const typename T::storage* __restrict__ Q, const typename T::storage* __restrict__ K,
@@ -285,7 +288,10 @@ __global__ __launch_bounds__(64 * decode_waves<NQ>()) void decode_kernel(
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int split = blockIdx.x % n_splits, wgh = blockIdx.x / n_splits;
+  const int lb = xcd_remap(blockIdx.x, gridDim.x);
+  const int gh = gq == 1 ? g.group : 1;                    // workgroups per K / V slice
+  const int gj = lb % gh, rest = lb / gh;
+  const int split = rest % n_splits, wgh = (rest / n_splits) * gh + gj;
   const int n_rows = gq * g.n_q;
   const int bhq0 = wgh * gq;                               // first q head of this workgroup
   const size_t qb = (size_t)bhq0 * g.n_q * D;
