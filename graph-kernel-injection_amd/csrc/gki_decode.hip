@@ -25,6 +25,10 @@
 // gfx950 write back and invalidate L2.
 // Numerics follow the reference forward: fp32 scores scaled after the dot, P
 // cast to V's dtype before P V, token mask causal & (sink | window).
+#include <atomic>
+#include <string>
+#include <type_traits>
+
 #include "gki_common.cuh"
 
 namespace gki {
@@ -481,6 +485,246 @@ int launch_decode(int dtype, int head_dim, const Geom& g, const void* q, const v
 #undef GKI_DECODE_CASE
 }
 
+// ---------------------------------------------------------------------------
+// Grouped-query decode on the matrix cores: one query position, 16-bit K / V,
+// head_dim 64 or 128, a group of 2..kDecodeMaxQ q heads per K / V stream. The
+// group's q heads are the B operand of S^T = K Q^T (16 columns, the unused
+// ones zero); each wave takes 16 tokens of every 64-token chunk of the
+// workgroup's slice of the stream; the chunk's K / V rows are gathered into
+// LDS by LDS-DMA (swizzled as the forward's tiles), so no registers hold loads
+// in flight and two chunks are requested at once. P^T of the wave's 16 tokens
+// is the B operand of O^T += V^T P^T (v_mfma_f32_16x16x16, V^T from one
+// transposed LDS read); the row sums add the fp32 P. The four waves' states
+// merge through LDS into the same partials / output as decode_kernel.
+// ---------------------------------------------------------------------------
+// One ds_read_b64_tr_b16: lane (g, c) gets tile[k0 + 4g + e][n0 + c], e = 0..3,
+// the K-operand layout of v_mfma_f32_16x16x16_{bf16,f16} for a K-major matrix.
+template <int D>
+__device__ inline uint2 lds_tr4(const uint16_t* tile, int k0, int n0, int lane) {
+  const int g = lane >> 4, l = lane & 15;
+  const uint16_t* p = tile + lds_off<D>(k0 + 4 * g + (l >> 2), n0 + 4 * (l & 3));
+  return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)p));
+}
+
+template <typename T>
+__device__ inline floatx4 mfma16k(const uint2& a, const uint2& b, floatx4 c) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  typedef _Float16 h16x4 __attribute__((ext_vector_type(4)));
+  if constexpr (std::is_same<T, BF16>::value)
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a),
+                                                     __builtin_bit_cast(s16x4, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h16x4, a),
+                                                 __builtin_bit_cast(h16x4, b), c, 0, 0, 0);
+}
+
+// s_waitcnt vmcnt(N), other counters untouched (N < 64: the field's low four
+// bits at 3:0, its high two at 15:14).
+template <int N>
+__device__ inline void vm_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt field");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
+// Chunks in flight per workgroup (LDS ring of K and V tiles).
+#ifndef GKI_DECODE_MFMA_BUFS
+#define GKI_DECODE_MFMA_BUFS 2
+#endif
+template <int D>
+constexpr int decode_mfma_bufs() { return GKI_DECODE_MFMA_BUFS; }
+template <int D>
+constexpr int decode_mfma_lds() { return 2 * decode_mfma_bufs<D>() * kTileN * D * 2; }
+
+// Wait until at most k chunks (of 2 * NP LDS-DMA instructions per wave each)
+// are still in flight.
+template <int NP, int NBUF>
+__device__ inline void wait_chunks(int k) {
+  static_assert(NBUF <= 4, "wait_chunks covers up to three chunks in flight");
+  if (k <= 0) vm_wait<0>();
+  else if (k == 1) vm_wait<2 * NP>();
+  else if (k == 2) vm_wait<(NBUF > 2 ? 4 * NP : 0)>();
+  else vm_wait<(NBUF > 3 ? 6 * NP : 0)>();
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void decode_mfma_kernel(
+    Geom g, const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+    const uint16_t* __restrict__ V, uint16_t* __restrict__ O, float* __restrict__ LSE,
+    float* __restrict__ ws, RingTokens src, int kv_rows, int n_tokens, int n_splits) {
+  static_assert(D == 64 || D == 128, "matrix-core decode: head_dim 64 or 128");
+  constexpr int KS = D / 32, DT = D / 16;
+  constexpr int NP = D / 32;                 // 1 KB LDS blocks per wave and 64-row tile
+  constexpr int NBUF = decode_mfma_bufs<D>();
+  extern __shared__ __align__(16) uint16_t decode_lds[];
+  uint16_t* const sk = decode_lds;                       // [NBUF][64 * D]
+  uint16_t* const sv = decode_lds + NBUF * kTileN * D;   // [NBUF][64 * D]
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = lane >> 4, col = lane & 15;
+  const int lb = xcd_remap(blockIdx.x, gridDim.x);
+  const int split = lb % n_splits, wgh = lb / n_splits;     // wgh: one K / V stream
+  const int n_rows = g.group;                               // n_q == 1: one row per q head
+  const int bhq0 = wgh * g.group;
+  const size_t qb = (size_t)bhq0 * D;
+  const size_t kb = (size_t)kv_bh(g, bhq0) * kv_rows * D;
+  const int g0 = (int)(((int64_t)n_tokens * split) / n_splits);
+  const int g1 = (int)(((int64_t)n_tokens * (split + 1)) / n_splits);
+  const int n_chunks = (g1 - g0 + kTileN - 1) / kTileN;
+
+  // Q^T operand: lane (grp, col) holds elements 32ks + 8grp .. +7 of q row col
+  uint4 qf[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks)
+    qf[ks] = col < n_rows ? *(const uint4*)(Q + qb + (size_t)col * D + 32 * ks + 8 * grp)
+                          : make_uint4(0, 0, 0, 0);
+  dma_wait();   // the Q loads are complete before any LDS-DMA is in flight
+
+  // this lane's chunk of LDS block 4p + wave of a tile: row, swizzled column
+  int drow[NP], dcol[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int e = (4 * p + wave) * 512 + 8 * lane;
+    drow[p] = e / D;
+    dcol[p] = (((e % D) >> 3) ^ lds_swz<D>(drow[p])) << 3;
+  }
+  // gather chunk c of the slice into buffer b (rows past the slice repeat its
+  // last token and are masked when consumed)
+  auto issue = [&](int c, int b) {
+    const int c0 = g0 + c * kTileN;
+    const uint32_t lk = lds_addr(sk + b * kTileN * D), lv = lds_addr(sv + b * kTileN * D);
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const int t = min(c0 + drow[p], g1 - 1);
+      const size_t off = kb + (size_t)src.row(src.entry(t)) * D + dcol[p];
+      dma_load16(K + off, lk + (4 * p + wave) * 1024);
+      dma_load16(V + off, lv + (4 * p + wave) * 1024);
+    }
+  };
+
+  floatx4 o[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) o[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float lsum = 0.f;                            // this lane's 4 tokens per chunk, row col
+  float m = kNegInf;
+
+#pragma unroll
+  for (int c = 0; c < NBUF; ++c)
+    if (c < n_chunks) issue(c, c);
+  for (int c = 0; c < n_chunks; ++c) {
+    const int b = c % NBUF;
+    // chunk c has landed; the up to NBUF - 1 chunks issued after it may stay in flight
+    wait_chunks<NP, NBUF>(min(NBUF - 1, n_chunks - 1 - c));
+    __syncthreads();
+    const uint16_t* ck = sk + b * kTileN * D;
+    const uint16_t* cv = sv + b * kTileN * D;
+    floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) s = T::mfma(lds_row8<D>(ck, 16 * wave + col, 32 * ks + 8 * grp), qf[ks], s);
+    // lane (grp, col): s[i] = score of token t0 + i for q row col
+    const int t0 = g0 + c * kTileN + 16 * wave + 4 * grp;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s[i] = t0 + i < g1 ? s[i] : kNegInf;
+    float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+    if (__any(mx * g.scale_log2 > m + kDecodeSlack)) {
+      mx = wave_max16x4(mx) * g.scale_log2;
+      const bool grow = mx > m + kDecodeSlack;
+      const float alpha = grow ? __builtin_amdgcn_exp2f(m - mx) : 1.f;
+      m = grow ? mx : m;
+      lsum *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+    }
+    const float m_use = m == kNegInf ? 0.f : m;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], g.scale_log2, -m_use));
+    lsum += (s[0] + s[1]) + (s[2] + s[3]);
+    const uint2 pb = make_uint2(pack2<T>(s[0], s[1]), pack2<T>(s[2], s[3]));
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o[dt] = mfma16k<T>(lds_tr4<D>(cv, 16 * wave, 16 * dt, lane), pb, o[dt]);
+    __syncthreads();                           // every wave is done with buffer b
+    if (c + NBUF < n_chunks) issue(c + NBUF, b);
+  }
+
+  // merge the four waves: lane (grp, col) holds O^T rows 16dt + 4grp + i of q row col
+  lsum = wave_sum16x4(lsum);
+  __syncthreads();
+  float* wacc = (float*)sk;                    // [4][16][D] (fits two K buffers)
+  float* wml = (float*)sv;                     // [4][16][2]
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wacc[(wave * 16 + col) * D + 16 * dt + 4 * grp + i] = o[dt][i];
+  if (grp == 0) {
+    wml[(wave * 16 + col) * 2] = m;
+    wml[(wave * 16 + col) * 2 + 1] = lsum;
+  }
+  __syncthreads();
+  const size_t row_stride = D + 2;
+  float* part = ws + ((size_t)wgh * n_splits + split) * n_rows * row_stride;
+  for (int idx = tid; idx < n_rows * D; idx += 256) {
+    const int r = idx / D, d = idx - r * D;
+    float M = kNegInf;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) M = fmaxf(M, wml[(w * 16 + r) * 2]);
+    const float Mu = M == kNegInf ? 0.f : M;
+    float L = 0.f, a = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float sw = __builtin_amdgcn_exp2f(wml[(w * 16 + r) * 2] - Mu);
+      L += wml[(w * 16 + r) * 2 + 1] * sw;
+      a += wacc[(w * 16 + r) * D + d] * sw;
+    }
+    if (n_splits == 1) {
+      const bool valid = L > 0.f;
+      O[qb + (size_t)r * D + d] = T::from_float(valid ? a / L : 0.f);
+      if (d == 0) LSE[(size_t)bhq0 + r] = valid ? M * kLn2 + __logf(L) : 0.f;
+    } else {
+      part[r * row_stride + d] = a;
+      if (d == 0) {
+        part[r * row_stride + D] = M;
+        part[r * row_stride + D + 1] = L;
+      }
+    }
+  }
+}
+
+// The matrix-core decode serves a grouped-query group of 2..kDecodeMaxQ q heads
+// at one query position (16-bit, head_dim 64 / 128): the case where
+// decode_heads_per_workgroup gives the whole group to one workgroup.
+inline bool decode_on_mfma(int dtype, int head_dim, const Geom& g) {
+  return dtype != kF32 && (head_dim == 64 || head_dim == 128) && g.n_q == 1 && g.group > 1 &&
+         decode_heads_per_workgroup(g.group, g.n_q) == g.group;
+}
+
+template <typename T, int D>
+int launch_decode_mfma(const Geom& g, const void* q, const void* k, const void* v, void* o, float* lse,
+                       const RingTokens& src, int kv_rows, int n_tokens, float* ws, int n_splits,
+                       hipStream_t stream, const char* what) {
+  const int n_wgh = g.B * g.H_kv;
+  constexpr int lds = decode_mfma_lds<D>();
+  if constexpr (lds > 65536) {
+    // above the 64 KB default: opt in once per device and instantiation
+    static std::atomic<uint64_t> done{0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return fail(3, std::string(what) + ": hipGetDevice failed");
+    const uint64_t bit = dev < 64 ? (1ull << dev) : 0;
+    if (!bit || !(done.load() & bit)) {
+      if (hipFuncSetAttribute((const void*)decode_mfma_kernel<T, D>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
+        return fail(3, std::string(what) + ": cannot reserve LDS for the matrix-core decode");
+      done.fetch_or(bit);
+    }
+  }
+  hipLaunchKernelGGL((decode_mfma_kernel<T, D>), dim3(n_wgh * n_splits), dim3(256), lds, stream, g,
+                     (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, lse, ws,
+                     src, kv_rows, n_tokens, n_splits);
+  if (n_splits > 1)
+    hipLaunchKernelGGL((combine_kernel<T, D>), dim3(n_wgh * g.group), dim3(64), 0, stream, ws,
+                       (uint16_t*)o, lse, g.group, n_splits);
+  return check_launch(what);
+}
+
 // Rolling-cache append: one thread per 16-byte chunk of the rows that survive
 // the call. Of the n_new appended positions start .. end-1, only sink positions
 // (< sink) and the last `ring` positions >= sink are written: earlier ones would
@@ -571,6 +815,14 @@ int decode_ring_dispatch(int dtype, int head_dim, const Geom& g, const void* q, 
   ring_stream(g.n_kv, g.n_q, g.sink, g.window, ring, &src.n_sink, &src.w_lo, &src.base, &n_tokens);
   src.sink = g.sink;
   src.ring = ring;
+  if (decode_on_mfma(dtype, head_dim, g)) {
+    const char* what = "gki_rolling_decode";
+    if (dtype == kF16)
+      return head_dim == 64 ? launch_decode_mfma<F16, 64>(g, q, k, v, o, lse, src, g.sink + ring, n_tokens, ws, n_splits, stream, what)
+                            : launch_decode_mfma<F16, 128>(g, q, k, v, o, lse, src, g.sink + ring, n_tokens, ws, n_splits, stream, what);
+    return head_dim == 64 ? launch_decode_mfma<BF16, 64>(g, q, k, v, o, lse, src, g.sink + ring, n_tokens, ws, n_splits, stream, what)
+                          : launch_decode_mfma<BF16, 128>(g, q, k, v, o, lse, src, g.sink + ring, n_tokens, ws, n_splits, stream, what);
+  }
   return launch_decode(dtype, head_dim, g, q, k, v, o, lse, src, g.sink + ring, n_tokens, ws, n_splits,
                        stream, "gki_rolling_decode");
 }

@@ -140,16 +140,20 @@ def test_gqa_prefill_fwd_bwd(B, H, H_kv, n_q, n_kv, D, bm, bn, S, W, dtype):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("H,H_kv,n_q,D,dtype", [
-    (8, 2, 1, 128, torch.bfloat16),     # 4 heads share one K/V stream
-    (8, 2, 2, 64, torch.float16),       # 4 x 2 rows > 4: one head per workgroup
-    (4, 1, 1, 64, torch.float32),       # MQA, 4 heads per stream
-    (6, 3, 2, 128, torch.bfloat16),     # 2 heads x 2 rows
-    (16, 2, 1, 128, torch.bfloat16),    # group 8 > 4 rows
+@pytest.mark.parametrize("H,H_kv,n_q,D,dtype,W", [
+    (8, 2, 1, 128, torch.bfloat16, 1024),   # 4 heads share one K/V stream (matrix cores, 4 splits)
+    (8, 4, 1, 64, torch.float16, 1024),     # group 2, head_dim 64 (matrix cores)
+    (4, 1, 1, 128, torch.float16, 1024),    # MQA, group 4 (matrix cores)
+    (8, 2, 1, 64, torch.bfloat16, 200),     # 204 tokens: one split, one ragged chunk
+    (8, 2, 1, 128, torch.float16, 100),     # 104 tokens: last chunk one wave partly, one fully masked
+    (8, 2, 2, 64, torch.float16, 1024),     # 4 x 2 rows > 4: one head per workgroup
+    (4, 1, 1, 64, torch.float32, 1024),     # MQA, 4 heads per stream (fp32: 4-row kernel)
+    (6, 3, 2, 128, torch.bfloat16, 1024),   # 2 heads x 2 rows
+    (16, 2, 1, 128, torch.bfloat16, 1024),  # group 8 > 4 rows
 ])
-def test_gqa_decode_and_rolling_cache(H, H_kv, n_q, D, dtype):
-    B, n_kv, S, W = 2, 5000, 4, 1024
-    tag = f"B{B} H{H}/{H_kv} nq{n_q} D{D} {dtype}"
+def test_gqa_decode_and_rolling_cache(H, H_kv, n_q, D, dtype, W):
+    B, n_kv, S = 2, 5000, 4
+    tag = f"B{B} H{H}/{H_kv} nq{n_q} D{D} {dtype} W{W}"
     print(f"[case] {tag}", flush=True)
     g = H // H_kv
     q, k, v, _ = _inputs(B, H, H_kv, n_q, n_kv, D, dtype, H + n_q)

@@ -230,7 +230,8 @@ def test_rolling_decode_steps_across_the_ring_wrap():
 def test_full_cache_decode_computes_the_stream(B, H, H_kv, n_q, n_kv, D, S, W, dtype):
     """A StreamingLLM mask's decode stream is computed in the kernel (the full
     cache decoded as a sink + ring cache, slot = position) instead of read from
-    the token list; both give the same bits. A custom mask keeps the list."""
+    the token list; both give the same bits where both run the same kernel. A
+    custom mask keeps the list."""
     print(f"[case] B{B} H{H}/{H_kv} nq{n_q} nkv{n_kv} D{D} S{S} W{W} {dtype}", flush=True)
     mask = stk.make_streaming_mask(n_q, n_kv, stk.StreamingMaskSpec(S, W), 1, 64, device=DEV)
     sched = decode_schedule(mask, n_q, n_kv, 1, 64, True, S, W)
@@ -256,7 +257,13 @@ def test_full_cache_decode_computes_the_stream(B, H, H_kv, n_q, n_kv, D, S, W, d
                                   ws.data_ptr() if n_splits > 1 else 0, n_splits,
                                   torch.cuda.current_stream().cuda_stream), "gki_bsa_decode")
     torch.cuda.synchronize()
-    assert torch.equal(o, o_list)
+    if dtype != torch.float32 and n_q == 1 and 1 < H // H_kv <= 4 and D in (64, 128):
+        # a 16-bit grouped-query step on the computed stream runs the matrix-core
+        # kernel, the list the 4-row kernel: the same stream (pinned bit for bit by
+        # the multi-head cases, which share the token source), other arithmetic
+        _close(o, o_list.float(), dtype, "computed vs listed stream")
+    else:
+        assert torch.equal(o, o_list)
     # a custom mask (one window block dropped) keeps the token list
     m2 = mask.clone()
     m2[0, -2] = 0
