@@ -487,7 +487,7 @@ int launch_decode(int dtype, int head_dim, const Geom& g, const void* q, const v
 
 // ---------------------------------------------------------------------------
 // Grouped-query decode on the matrix cores: one query position, 16-bit K / V,
-// head_dim 64 or 128, a group of 2..kDecodeMaxQ q heads per K / V stream. The
+// head_dim 64 or 128, a group of 2..kDecodeTileM q heads per K / V stream. The
 // group's q heads are the B operand of S^T = K Q^T (16 columns, the unused
 // ones zero); each wave takes 16 tokens of every 64-token chunk of the
 // workgroup's slice of the stream; the chunk's K / V rows are gathered into
@@ -689,12 +689,12 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(
   }
 }
 
-// The matrix-core decode serves a grouped-query group of 2..kDecodeMaxQ q heads
-// at one query position (16-bit, head_dim 64 / 128): the case where
-// decode_heads_per_workgroup gives the whole group to one workgroup.
+// The matrix-core decode serves a grouped-query group of 2..kDecodeTileM q heads
+// at one query position (16-bit, head_dim 64 / 128), the whole group in one
+// workgroup (one K / V read per group).
 inline bool decode_on_mfma(int dtype, int head_dim, const Geom& g) {
   return dtype != kF32 && (head_dim == 64 || head_dim == 128) && g.n_q == 1 && g.group > 1 &&
-         decode_heads_per_workgroup(g.group, g.n_q) == g.group;
+         g.group <= kDecodeTileM;
 }
 
 template <typename T, int D>

@@ -31,9 +31,8 @@ import torch
 
 from . import _lib
 from .masks import StreamingMaskSpec
-from .ops import _aligned, _decode_slots, _decode_splits
+from .ops import _DTYPE_CODE, _aligned, _decode_on_mfma, _decode_slots, _decode_splits
 
-_DTYPE_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 _DECODE_HEAD_DIMS = (64, 128)
 
 
@@ -150,8 +149,10 @@ class StreamingKVCache:
         _, _, n_tokens = rolling_stream(self.length, n_q, self.sink_size, self.window_size,
                                         self.ring_size)
         B, H, H_kv = self.batch, int(q.shape[1]), self.heads
-        n_splits = _decode_splits(n_tokens, _decode_slots(B, H, H_kv, n_q,
-                                                          _lib.tile_sizes()["decode_max_q"]))
+        ts = _lib.tile_sizes()
+        mfma = _decode_on_mfma(_DTYPE_CODE[self.dtype], self.head_dim, H // H_kv, n_q,
+                               ts["decode_tile_m"])
+        n_splits = _decode_splits(n_tokens, _decode_slots(B, H, H_kv, n_q, ts["decode_max_q"], mfma))
         o = torch.empty_like(q)
         lse = torch.empty((B, H, n_q), dtype=torch.float32, device=self.device)
         lib = _lib.load()

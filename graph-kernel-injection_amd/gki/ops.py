@@ -58,10 +58,20 @@ def _decode_splits(n_tokens: int, bh: int) -> int:
     return max(1, min(want, cap))
 
 
-def _decode_slots(B: int, H: int, H_kv: int, n_q: int, max_q: int) -> int:
-    """(b, head) slots of the decode grid: a grouped-query group's q heads share
-    one workgroup when group * n_q fits the kernel's rows (the library's
+def _decode_on_mfma(dtype_code: int, D: int, group: int, n_q: int, max_rows: int) -> bool:
+    """The library's ``decode_on_mfma`` rule: a computed-stream decode of 2 ..
+    ``max_rows`` (decode_tile_m) q heads per K / V stream at one query position,
+    16-bit, head_dim 64 / 128, runs on the matrix cores, one workgroup per group."""
+    return dtype_code != 0 and D in (64, 128) and n_q == 1 and 1 < group <= max_rows
+
+
+def _decode_slots(B: int, H: int, H_kv: int, n_q: int, max_q: int, mfma: bool = False) -> int:
+    """(b, head) slots of the decode grid: one per K / V stream on the matrix
+    cores (``mfma``); else a grouped-query group's q heads share one workgroup
+    when group * n_q fits the kernel's rows (the library's
     ``decode_heads_per_workgroup`` rule), else one q head per workgroup."""
+    if mfma:
+        return B * H_kv
     group = H // H_kv
     gq = group if group > 1 and group * n_q <= max_q else 1
     return B * H // gq
@@ -133,8 +143,10 @@ class _BlockSparseFlashAttention(torch.autograd.Function):
             if N_Q <= ts["decode_max_q"] and D in _DECODE_HEAD_DIMS:
                 sched = decode_schedule(block_mask, N_Q, N_KV, block_m, block_n, bool(is_causal),
                                         int(sink_size), int(window_size))
+                mfma = bool(sched.ring) and _decode_on_mfma(dtype, D, H // H_kv, N_Q,
+                                                            ts["decode_tile_m"])
                 n_splits = _decode_splits(sched.n_tokens,
-                                          _decode_slots(B, H, H_kv, N_Q, ts["decode_max_q"]))
+                                          _decode_slots(B, H, H_kv, N_Q, ts["decode_max_q"], mfma))
                 ws_ptr = 0
                 if n_splits > 1:
                     ws = torch.empty(int(lib.gki_bsa_decode_workspace_floats(B, H, N_Q, D, n_splits)),

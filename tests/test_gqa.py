@@ -149,7 +149,9 @@ def test_gqa_prefill_fwd_bwd(B, H, H_kv, n_q, n_kv, D, bm, bn, S, W, dtype):
     (8, 2, 2, 64, torch.float16, 1024),     # 4 x 2 rows > 4: one head per workgroup
     (4, 1, 1, 64, torch.float32, 1024),     # MQA, 4 heads per stream (fp32: 4-row kernel)
     (6, 3, 2, 128, torch.bfloat16, 1024),   # 2 heads x 2 rows
-    (16, 2, 1, 128, torch.bfloat16, 1024),  # group 8 > 4 rows
+    (16, 2, 1, 128, torch.bfloat16, 1024),  # group 8 (matrix cores: 8 of 16 columns)
+    (32, 2, 1, 64, torch.float16, 1024),    # group 16: all 16 columns
+    (32, 1, 1, 128, torch.bfloat16, 1024),  # group 32 > 16: one head per workgroup, shared L2
 ])
 def test_gqa_decode_and_rolling_cache(H, H_kv, n_q, D, dtype, W):
     B, n_kv, S = 2, 5000, 4

@@ -257,7 +257,7 @@ def test_full_cache_decode_computes_the_stream(B, H, H_kv, n_q, n_kv, D, S, W, d
                                   ws.data_ptr() if n_splits > 1 else 0, n_splits,
                                   torch.cuda.current_stream().cuda_stream), "gki_bsa_decode")
     torch.cuda.synchronize()
-    if dtype != torch.float32 and n_q == 1 and 1 < H // H_kv <= 4 and D in (64, 128):
+    if dtype != torch.float32 and n_q == 1 and 1 < H // H_kv <= 16 and D in (64, 128):
         # a 16-bit grouped-query step on the computed stream runs the matrix-core
         # kernel, the list the 4-row kernel: the same stream (pinned bit for bit by
         # the multi-head cases, which share the token source), other arithmetic
