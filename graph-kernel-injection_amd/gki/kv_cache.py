@@ -31,7 +31,8 @@ import torch
 
 from . import _lib
 from .masks import StreamingMaskSpec
-from .ops import _DTYPE_CODE, _aligned, _decode_on_mfma, _decode_slots, _decode_splits
+from .ops import (_DTYPE_CODE, _aligned, _current_stream, _decode_on_mfma, _decode_slots,
+                  _decode_splits, _on_device)
 
 _DECODE_HEAD_DIMS = (64, 128)
 
@@ -123,8 +124,8 @@ class StreamingKVCache:
             return
         k, v = _aligned(k), _aligned(v)
         lib = _lib.load()
-        with torch.cuda.device(self.device):
-            stream = torch.cuda.current_stream(self.device).cuda_stream
+        with _on_device(self.device):
+            stream = _current_stream(self.device)
             _lib.check(lib.gki_rolling_append(
                 self.k_cache.data_ptr(), self.v_cache.data_ptr(), k.data_ptr(), v.data_ptr(),
                 _DTYPE_CODE[self.dtype], self.batch, self.heads, self.head_dim, self.sink_size,
@@ -156,8 +157,8 @@ class StreamingKVCache:
         o = torch.empty_like(q)
         lse = torch.empty((B, H, n_q), dtype=torch.float32, device=self.device)
         lib = _lib.load()
-        with torch.cuda.device(self.device):
-            stream = torch.cuda.current_stream(self.device).cuda_stream
+        with _on_device(self.device):
+            stream = _current_stream(self.device)
             ws_ptr = 0
             if n_splits > 1:
                 ws = torch.empty(int(lib.gki_bsa_decode_workspace_floats(B, H, n_q, self.head_dim,

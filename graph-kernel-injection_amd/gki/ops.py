@@ -17,6 +17,7 @@ There is no CPU or eager fallback: a missing library raises ``RuntimeError``.
 
 from __future__ import annotations
 
+import contextlib
 import math
 from typing import Optional, Tuple
 
@@ -50,6 +51,19 @@ def _device_mask(block_mask: torch.Tensor, device: torch.device) -> torch.Tensor
     return block_mask.to(device=device, dtype=torch.int32).contiguous()
 
 
+def _current_stream(dev: torch.device) -> int:
+    """Raw handle of ``dev``'s current stream (torch's stream query without its
+    Python wrapper when available)."""
+    raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+    return raw(dev.index) if raw is not None else torch.cuda.current_stream(dev).cuda_stream
+
+
+def _on_device(dev: torch.device):
+    """``dev`` as the current device for the launches (a no-op context when it
+    already is)."""
+    return contextlib.nullcontext() if dev.index == torch.cuda.current_device() else torch.cuda.device(dev)
+
+
 def _decode_splits(n_tokens: int, bh: int) -> int:
     """Decode workgroups per (b, head) slot: about one per CU in total, but at
     least ~256 tokens (a few rounds per wave) per workgroup."""
@@ -77,6 +91,89 @@ def _decode_slots(B: int, H: int, H_kv: int, n_q: int, max_q: int, mfma: bool = 
     return B * H // gq
 
 
+def _attention_forward(q, k, v, block_mask, softmax_scale, block_m, block_n, is_causal, sink_size,
+                       window_size, enable_gqa):
+    """Validation and the forward launch (``sparse_triton_kernel.py:615-682``):
+    returns (o, lse, q, k, v, block_mask, q_offset) with q / k / v / block_mask
+    as the kernels read them (16-byte aligned, int32 mask on q's device)."""
+    lib = _lib.load()
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("Q/K/V must be 4-D [B, H, N, D] tensors")
+    if not (q.is_cuda and k.is_cuda and v.is_cuda):
+        raise ValueError("All inputs must live on a CUDA device")
+
+    B, H, N_Q, D = q.shape
+    N_KV = k.shape[2]
+    if k.shape != v.shape:
+        raise ValueError("K and V must share shape")
+    H_kv = k.shape[1]
+    heads_ok = H_kv == H or (enable_gqa and H_kv > 0 and H % H_kv == 0)
+    if k.shape[0] != B or not heads_ok or k.shape[-1] != D:
+        raise ValueError("Q/K/V batch/head/dim mismatch")
+    if not (q.dtype == k.dtype == v.dtype) or q.dtype not in _DTYPE_CODE:
+        raise ValueError(
+            f"Q/K/V must share one dtype among float32/float16/bfloat16, got "
+            f"{q.dtype}/{k.dtype}/{v.dtype}")
+    if D not in _HEAD_DIMS:
+        raise ValueError(f"head_dim must be one of {_HEAD_DIMS}, got {D}")
+
+    block_m, block_n = int(block_m), int(block_n)
+    n_qb = (N_Q + block_m - 1) // block_m
+    n_kb = (N_KV + block_n - 1) // block_n
+    if block_mask.shape != (n_qb, n_kb):
+        raise ValueError(
+            f"block_mask has shape {tuple(block_mask.shape)}, "
+            f"expected {(n_qb, n_kb)}"
+        )
+    q, k, v = _aligned(q), _aligned(k), _aligned(v)
+    dev = q.device
+    block_mask = _device_mask(block_mask, dev)
+
+    o = torch.empty_like(q)
+    lse = torch.empty((B, H, N_Q), dtype=torch.float32, device=dev)
+    q_offset = N_KV - N_Q
+    dtype = _DTYPE_CODE[q.dtype]
+    common = (block_mask.data_ptr(), n_qb, n_kb, block_m, block_n, float(softmax_scale),
+              int(bool(is_causal)), int(sink_size), int(window_size))
+
+    with _on_device(dev):
+        stream = _current_stream(dev)
+        ts = _lib.tile_sizes()
+        if N_Q <= ts["decode_max_q"] and D in _DECODE_HEAD_DIMS:
+            sched = decode_schedule(block_mask, N_Q, N_KV, block_m, block_n, bool(is_causal),
+                                    int(sink_size), int(window_size))
+            mfma = bool(sched.ring) and _decode_on_mfma(dtype, D, H // H_kv, N_Q,
+                                                        ts["decode_tile_m"])
+            n_splits = _decode_splits(sched.n_tokens,
+                                      _decode_slots(B, H, H_kv, N_Q, ts["decode_max_q"], mfma))
+            ws_ptr = 0
+            if n_splits > 1:
+                ws = torch.empty(int(lib.gki_bsa_decode_workspace_floats(B, H, N_Q, D, n_splits)),
+                                 dtype=torch.float32, device=dev)
+                ws_ptr = ws.data_ptr()
+            if sched.ring:
+                # the stream is the StreamingLLM one: positions computed in
+                # the kernel (no list read), same stream and arithmetic
+                _lib.check(lib.gki_rolling_decode(
+                    q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                    dtype, B, H, H_kv, N_Q, D, int(sink_size), int(window_size), sched.ring,
+                    N_KV, float(softmax_scale), ws_ptr, n_splits, stream), "gki_rolling_decode")
+            else:
+                _lib.check(lib.gki_bsa_decode(
+                    q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), dtype,
+                    B, H, H_kv, N_Q, N_KV, D, sched.tokens.data_ptr(), sched.n_tokens, *common,
+                    ws_ptr, n_splits, stream), "gki_bsa_decode")
+        else:
+            sched = fwd_schedule(block_mask, N_Q, N_KV, block_m, block_n, bool(is_causal),
+                                 int(sink_size), int(window_size), q.dtype == torch.float32)
+            _lib.check(lib.gki_bsa_fwd(
+                q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), dtype,
+                B, H, H_kv, N_Q, N_KV, D, sched.lists.row_ptr.data_ptr(),
+                sched.lists.row_idx.data_ptr(), sched.n_qt, *common, stream), "gki_bsa_fwd")
+
+    return o, lse, q, k, v, block_mask, q_offset
+
+
 class _BlockSparseFlashAttention(torch.autograd.Function):
     """Autograd bridge between PyTorch and the gfx950 kernels."""
 
@@ -97,81 +194,9 @@ class _BlockSparseFlashAttention(torch.autograd.Function):
     ) -> torch.Tensor:
         # extra = (enable_gqa,) when given: K / V may have H_kv heads dividing H
         enable_gqa = bool(extra[0]) if extra else False
-        lib = _lib.load()
-        if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
-            raise ValueError("Q/K/V must be 4-D [B, H, N, D] tensors")
-        if not (q.is_cuda and k.is_cuda and v.is_cuda):
-            raise ValueError("All inputs must live on a CUDA device")
-
-        B, H, N_Q, D = q.shape
-        N_KV = k.shape[2]
-        if k.shape != v.shape:
-            raise ValueError("K and V must share shape")
-        H_kv = k.shape[1]
-        heads_ok = H_kv == H or (enable_gqa and H_kv > 0 and H % H_kv == 0)
-        if k.shape[0] != B or not heads_ok or k.shape[-1] != D:
-            raise ValueError("Q/K/V batch/head/dim mismatch")
-        if not (q.dtype == k.dtype == v.dtype) or q.dtype not in _DTYPE_CODE:
-            raise ValueError(
-                f"Q/K/V must share one dtype among float32/float16/bfloat16, got "
-                f"{q.dtype}/{k.dtype}/{v.dtype}")
-        if D not in _HEAD_DIMS:
-            raise ValueError(f"head_dim must be one of {_HEAD_DIMS}, got {D}")
-
-        block_m, block_n = int(block_m), int(block_n)
-        n_qb = (N_Q + block_m - 1) // block_m
-        n_kb = (N_KV + block_n - 1) // block_n
-        if block_mask.shape != (n_qb, n_kb):
-            raise ValueError(
-                f"block_mask has shape {tuple(block_mask.shape)}, "
-                f"expected {(n_qb, n_kb)}"
-            )
-        q, k, v = _aligned(q), _aligned(k), _aligned(v)
-        dev = q.device
-        block_mask = _device_mask(block_mask, dev)
-
-        o = torch.empty_like(q)
-        lse = torch.empty((B, H, N_Q), dtype=torch.float32, device=dev)
-        q_offset = N_KV - N_Q
-        dtype = _DTYPE_CODE[q.dtype]
-        common = (block_mask.data_ptr(), n_qb, n_kb, block_m, block_n, float(softmax_scale),
-                  int(bool(is_causal)), int(sink_size), int(window_size))
-
-        with torch.cuda.device(dev):
-            stream = torch.cuda.current_stream(dev).cuda_stream
-            ts = _lib.tile_sizes()
-            if N_Q <= ts["decode_max_q"] and D in _DECODE_HEAD_DIMS:
-                sched = decode_schedule(block_mask, N_Q, N_KV, block_m, block_n, bool(is_causal),
-                                        int(sink_size), int(window_size))
-                mfma = bool(sched.ring) and _decode_on_mfma(dtype, D, H // H_kv, N_Q,
-                                                            ts["decode_tile_m"])
-                n_splits = _decode_splits(sched.n_tokens,
-                                          _decode_slots(B, H, H_kv, N_Q, ts["decode_max_q"], mfma))
-                ws_ptr = 0
-                if n_splits > 1:
-                    ws = torch.empty(int(lib.gki_bsa_decode_workspace_floats(B, H, N_Q, D, n_splits)),
-                                     dtype=torch.float32, device=dev)
-                    ws_ptr = ws.data_ptr()
-                if sched.ring:
-                    # the stream is the StreamingLLM one: positions computed in
-                    # the kernel (no list read), same stream and arithmetic
-                    _lib.check(lib.gki_rolling_decode(
-                        q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
-                        dtype, B, H, H_kv, N_Q, D, int(sink_size), int(window_size), sched.ring,
-                        N_KV, float(softmax_scale), ws_ptr, n_splits, stream), "gki_rolling_decode")
-                else:
-                    _lib.check(lib.gki_bsa_decode(
-                        q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), dtype,
-                        B, H, H_kv, N_Q, N_KV, D, sched.tokens.data_ptr(), sched.n_tokens, *common,
-                        ws_ptr, n_splits, stream), "gki_bsa_decode")
-            else:
-                sched = fwd_schedule(block_mask, N_Q, N_KV, block_m, block_n, bool(is_causal),
-                                     int(sink_size), int(window_size), q.dtype == torch.float32)
-                _lib.check(lib.gki_bsa_fwd(
-                    q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), dtype,
-                    B, H, H_kv, N_Q, N_KV, D, sched.lists.row_ptr.data_ptr(),
-                    sched.lists.row_idx.data_ptr(), sched.n_qt, *common, stream), "gki_bsa_fwd")
-
+        o, lse, q, k, v, block_mask, q_offset = _attention_forward(
+            q, k, v, block_mask, softmax_scale, block_m, block_n, is_causal, sink_size, window_size,
+            enable_gqa)
         ctx.save_for_backward(q, k, v, o, lse, block_mask)
         ctx.softmax_scale = softmax_scale
         ctx.block_m = block_m
@@ -252,6 +277,10 @@ def block_sparse_attention(
         softmax_scale = 1.0 / math.sqrt(q.shape[-1])
     args = (q.contiguous(), k.contiguous(), v.contiguous(), block_mask, float(softmax_scale),
             int(block_m), int(block_n), bool(is_causal), int(sink_size), int(window_size))
+    if not (torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad)):
+        # nothing to differentiate (inference, a decode step): the same forward
+        # without the autograd node and its saved tensors
+        return _attention_forward(*args, enable_gqa)[0]
     if enable_gqa:
         args += (True,)
     return _BlockSparseFlashAttention.apply(*args)
