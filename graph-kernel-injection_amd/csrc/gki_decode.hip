@@ -412,13 +412,17 @@ __global__ __launch_bounds__(64) void combine_kernel(const float* __restrict__ w
   const size_t row_stride = D + 2;
   const float* base = ws + (size_t)bh * n_splits * n_q * row_stride + (size_t)r * row_stride;
   const size_t sstride = (size_t)n_q * row_stride;
+  // unrolled so that several splits' loads are in flight at once (the
+  // partials were just written by other CUs: every load goes past this L2)
   float M = kNegInf;
+#pragma unroll 4
   for (int s = 0; s < n_splits; ++s) M = fmaxf(M, base[s * sstride + D]);
   const float Mu = M == kNegInf ? 0.f : M;
   float L = 0.f;
   float a[D / 64];
 #pragma unroll
   for (int j = 0; j < D / 64; ++j) a[j] = 0.f;
+#pragma unroll 4
   for (int s = 0; s < n_splits; ++s) {
     const float* ps = base + s * sstride;
     const float w = __builtin_amdgcn_exp2f(ps[D] - Mu);
