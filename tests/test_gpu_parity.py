@@ -430,6 +430,26 @@ def test_fwd_bwd_deterministic():
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("n_q", [1, 300])
+def test_inference_path_equals_the_autograd_forward(n_q):
+    """Without any input requiring a gradient (or under no_grad) the op runs the
+    forward without an autograd node: the same bits as the differentiable call,
+    and an output that does not require grad. Decode (n_q 1, grouped-query) and
+    prefill."""
+    B, H, H_kv, N, D = 1, 8, 2, 2000, 128
+    q, k, v, _ = _inputs((B, H, n_q, D), (B, H_kv, N, D), torch.bfloat16, seed=41)
+    mask = stk.make_streaming_mask(n_q, N, stk.StreamingMaskSpec(4, 256), 64, 64, device=DEV)
+    kw = dict(block_m=64, block_n=64, is_causal=True, sink_size=4, window_size=256, enable_gqa=True)
+    o_fast = stk.block_sparse_attention(q, k, v, mask, **kw)
+    with torch.no_grad():
+        o_nograd = stk.block_sparse_attention(q, k, v, mask, **kw)
+    leaves = [t.clone().requires_grad_(True) for t in (q, k, v)]
+    o_grad = stk.block_sparse_attention(*leaves, mask, **kw)
+    assert o_grad.requires_grad and o_grad.grad_fn is not None
+    assert not o_fast.requires_grad and o_fast.grad_fn is None
+    assert torch.equal(o_fast, o_grad.detach()) and torch.equal(o_nograd, o_fast)
+
+
 def test_misaligned_views_are_copied_not_faulted():
     """Contiguous views at an odd storage offset (2 bytes off a 16-byte
     boundary) give exactly the aligned result, forward and backward."""
