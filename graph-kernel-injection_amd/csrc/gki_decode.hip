@@ -490,10 +490,10 @@ int launch_decode(int dtype, int head_dim, const Geom& g, const void* q, const v
 }
 
 // ---------------------------------------------------------------------------
-// Grouped-query decode on the matrix cores: one query position, 16-bit K / V,
-// head_dim 64 or 128, a group of 2..kDecodeTileM q heads per K / V stream. The
-// group's q heads are the B operand of S^T = K Q^T (16 columns, the unused
-// ones zero); each wave takes 16 tokens of every 64-token chunk of the
+// Decode on the matrix cores: 16-bit K / V, head_dim 64 or 128, the n_q query
+// rows of a group's q heads (2..kDecodeTileM rows per K / V stream). Those rows
+// are the B operand of S^T = K Q^T (16 columns, the unused ones zero); with
+// several query positions (EXACT false) each row applies the token rule; each wave takes 16 tokens of every 64-token chunk of the
 // workgroup's slice of the stream; the chunk's K / V rows are gathered into
 // LDS by LDS-DMA (swizzled as the forward's tiles), so no registers hold loads
 // in flight and two chunks are requested at once. P^T of the wave's 16 tokens
@@ -550,7 +550,7 @@ __device__ inline void wait_chunks(int k) {
   else vm_wait<(NBUF > 3 ? 6 * NP : 0)>();
 }
 
-template <typename T, int D>
+template <typename T, int D, bool EXACT>
 __global__ __launch_bounds__(256) void decode_mfma_kernel(
     Geom g, const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const uint16_t* __restrict__ V, uint16_t* __restrict__ O, float* __restrict__ LSE,
@@ -568,9 +568,10 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(
   const int grp = lane >> 4, col = lane & 15;
   const int lb = xcd_remap(blockIdx.x, gridDim.x);
   const int split = lb % n_splits, wgh = lb / n_splits;     // wgh: one K / V stream
-  const int n_rows = g.group;                               // n_q == 1: one row per q head
+  const int n_rows = g.group * g.n_q;                       // row r: q head r / n_q, query r % n_q
   const int bhq0 = wgh * g.group;
-  const size_t qb = (size_t)bhq0 * D;
+  const size_t qb = (size_t)bhq0 * g.n_q * D;
+  const int my_q = col % g.n_q;                             // this lane's query row
   const size_t kb = (size_t)kv_bh(g, bhq0) * kv_rows * D;
   const int g0 = (int)(((int64_t)n_tokens * split) / n_splits);
   const int g1 = (int)(((int64_t)n_tokens * (split + 1)) / n_splits);
@@ -628,7 +629,12 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(
     // lane (grp, col): s[i] = score of token t0 + i for q row col
     const int t0 = g0 + c * kTileN + 16 * wave + 4 * grp;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) s[i] = t0 + i < g1 ? s[i] : kNegInf;
+    for (int i = 0; i < 4; ++i) {
+      bool ok = t0 + i < g1;
+      if constexpr (!EXACT)   // several query positions: the token rule per row
+        ok = ok && elem_tok(g, my_q, src.entry(min(t0 + i, g1 - 1)) & kIdxMask);
+      s[i] = ok ? s[i] : kNegInf;
+    }
     float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
     if (__any(mx * g.scale_log2 > m + kDecodeSlack)) {
       mx = wave_max16x4(mx) * g.scale_log2;
@@ -682,7 +688,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(
     if (n_splits == 1) {
       const bool valid = L > 0.f;
       O[qb + (size_t)r * D + d] = T::from_float(valid ? a / L : 0.f);
-      if (d == 0) LSE[(size_t)bhq0 + r] = valid ? M * kLn2 + __logf(L) : 0.f;
+      if (d == 0) LSE[(size_t)bhq0 * g.n_q + r] = valid ? M * kLn2 + __logf(L) : 0.f;
     } else {
       part[r * row_stride + d] = a;
       if (d == 0) {
@@ -693,12 +699,12 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(
   }
 }
 
-// The matrix-core decode serves a grouped-query group of 2..kDecodeTileM q heads
-// at one query position (16-bit, head_dim 64 / 128), the whole group in one
-// workgroup (one K / V read per group).
+// The matrix-core decode serves the group * n_q query rows of a K / V stream
+// when they are 2..kDecodeTileM (16-bit, head_dim 64 / 128), the whole group in
+// one workgroup (one K / V read per group); a single row keeps decode_kernel.
 inline bool decode_on_mfma(int dtype, int head_dim, const Geom& g) {
-  return dtype != kF32 && (head_dim == 64 || head_dim == 128) && g.n_q == 1 && g.group > 1 &&
-         g.group <= kDecodeTileM;
+  const int rows = g.group * g.n_q;
+  return dtype != kF32 && (head_dim == 64 || head_dim == 128) && rows >= 2 && rows <= kDecodeTileM;
 }
 
 template <typename T, int D>
@@ -714,18 +720,26 @@ int launch_decode_mfma(const Geom& g, const void* q, const void* k, const void* 
     if (hipGetDevice(&dev) != hipSuccess) return fail(3, std::string(what) + ": hipGetDevice failed");
     const uint64_t bit = dev < 64 ? (1ull << dev) : 0;
     if (!bit || !(done.load() & bit)) {
-      if (hipFuncSetAttribute((const void*)decode_mfma_kernel<T, D>,
+      if (hipFuncSetAttribute((const void*)decode_mfma_kernel<T, D, true>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess ||
+          hipFuncSetAttribute((const void*)decode_mfma_kernel<T, D, false>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
         return fail(3, std::string(what) + ": cannot reserve LDS for the matrix-core decode");
       done.fetch_or(bit);
     }
   }
-  hipLaunchKernelGGL((decode_mfma_kernel<T, D>), dim3(n_wgh * n_splits), dim3(256), lds, stream, g,
-                     (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, lse, ws,
-                     src, kv_rows, n_tokens, n_splits);
+  if (g.n_q == 1)
+    hipLaunchKernelGGL((decode_mfma_kernel<T, D, true>), dim3(n_wgh * n_splits), dim3(256), lds, stream,
+                       g, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, lse,
+                       ws, src, kv_rows, n_tokens, n_splits);
+  else
+    hipLaunchKernelGGL((decode_mfma_kernel<T, D, false>), dim3(n_wgh * n_splits), dim3(256), lds, stream,
+                       g, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, lse,
+                       ws, src, kv_rows, n_tokens, n_splits);
+  const int n_rows = g.group * g.n_q;
   if (n_splits > 1)
-    hipLaunchKernelGGL((combine_kernel<T, D>), dim3(n_wgh * g.group), dim3(64), 0, stream, ws,
-                       (uint16_t*)o, lse, g.group, n_splits);
+    hipLaunchKernelGGL((combine_kernel<T, D>), dim3(n_wgh * n_rows), dim3(64), 0, stream, ws,
+                       (uint16_t*)o, lse, n_rows, n_splits);
   return check_launch(what);
 }
 

@@ -120,6 +120,12 @@ def _close(ours, ref, dtype, what):
     assert not bad.any(), f"{what}: {int(bad.sum())} elements out of tolerance, max err {(o - r).abs().max():.3e}"
 
 
+def _on_matrix_cores(dtype, D, group, n_q):
+    """The library's rule for the matrix-core decode of a computed stream
+    (16-bit, head_dim 64 / 128, 2..16 query rows per K / V stream)."""
+    return dtype != torch.float32 and D in (64, 128) and 2 <= group * n_q <= 16
+
+
 def _full_cache_decode(q, k, v, sink, window):
     """The full-cache decode path (block_m = 1, block_n = 64, token rule) and
     the length of the token stream it walks."""
@@ -187,7 +193,14 @@ def test_rolling_decode_matches_full_cache_and_oracle(B, H, D, dtype, sink, wind
     o, lse = cache.attend(q, return_lse=True)
     o_full, n_full = _full_cache_decode(q, k, v, sink, window)
     n_roll = rolling_stream(length, n_q, sink, window, cache.ring_size)[2]
-    if n_roll == n_full:
+    listed = decode_schedule(stk.make_streaming_mask(n_q, length, stk.StreamingMaskSpec(sink, window), 1,
+                                                     64, device=DEV), n_q, length, 1, 64, True, sink,
+                             window).ring == 0
+    if n_roll == n_full and listed and _on_matrix_cores(dtype, D, 1, n_q):
+        # a full cache too short for the computed stream decodes its list with
+        # the 4-row kernel, the rolling cache on the matrix cores
+        _close(o, o_full.float(), dtype, "rolling vs full cache " + tag)
+    elif n_roll == n_full:
         assert torch.equal(o, o_full), tag
     o_ref, lse_ref = _oracle(q, k, v, sink, window)
     _close(o, o_ref, dtype, "O " + tag)
@@ -257,10 +270,11 @@ def test_full_cache_decode_computes_the_stream(B, H, H_kv, n_q, n_kv, D, S, W, d
                                   ws.data_ptr() if n_splits > 1 else 0, n_splits,
                                   torch.cuda.current_stream().cuda_stream), "gki_bsa_decode")
     torch.cuda.synchronize()
-    if dtype != torch.float32 and n_q == 1 and 1 < H // H_kv <= 16 and D in (64, 128):
-        # a 16-bit grouped-query step on the computed stream runs the matrix-core
-        # kernel, the list the 4-row kernel: the same stream (pinned bit for bit by
-        # the multi-head cases, which share the token source), other arithmetic
+    if _on_matrix_cores(dtype, D, H // H_kv, n_q):
+        # 2..16 query rows per K / V stream on the computed stream run the
+        # matrix-core kernel, the list the 4-row kernel: the same stream (pinned
+        # bit for bit by the single-row and fp32 cases, which share the token
+        # source), other arithmetic
         _close(o, o_list.float(), dtype, "computed vs listed stream")
     else:
         assert torch.equal(o, o_list)
