@@ -491,8 +491,9 @@ int launch_decode(int dtype, int head_dim, const Geom& g, const void* q, const v
 
 // ---------------------------------------------------------------------------
 // Decode on the matrix cores: 16-bit K / V, head_dim 64 or 128, the n_q query
-// rows of a group's q heads (2..kDecodeTileM rows per K / V stream). Those rows
-// are the B operand of S^T = K Q^T (16 columns, the unused ones zero); with
+// rows of a group's q heads (2 .. 2 * kDecodeTileM rows per K / V stream). Those
+// rows are the B operand of S^T = K Q^T (NB blocks of 16 columns, the unused
+// ones zero); with
 // several query positions (EXACT false) each row applies the token rule; each wave takes 16 tokens of every 64-token chunk of the
 // workgroup's slice of the stream; the chunk's K / V rows are gathered into
 // LDS by LDS-DMA (swizzled as the forward's tiles), so no registers hold loads
@@ -550,7 +551,7 @@ __device__ inline void wait_chunks(int k) {
   else vm_wait<(NBUF > 3 ? 6 * NP : 0)>();
 }
 
-template <typename T, int D, bool EXACT>
+template <typename T, int D, bool EXACT, int NB>
 __global__ __launch_bounds__(256) void decode_mfma_kernel(
     Geom g, const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const uint16_t* __restrict__ V, uint16_t* __restrict__ O, float* __restrict__ LSE,
@@ -571,18 +572,24 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(
   const int n_rows = g.group * g.n_q;                       // row r: q head r / n_q, query r % n_q
   const int bhq0 = wgh * g.group;
   const size_t qb = (size_t)bhq0 * g.n_q * D;
-  const int my_q = col % g.n_q;                             // this lane's query row
   const size_t kb = (size_t)kv_bh(g, bhq0) * kv_rows * D;
   const int g0 = (int)(((int64_t)n_tokens * split) / n_splits);
   const int g1 = (int)(((int64_t)n_tokens * (split + 1)) / n_splits);
   const int n_chunks = (g1 - g0 + kTileN - 1) / kTileN;
 
-  // Q^T operand: lane (grp, col) holds elements 32ks + 8grp .. +7 of q row col
-  uint4 qf[KS];
+  // Q^T operand of column block h: lane (grp, col) holds elements 32ks + 8grp ..
+  // +7 of q row 16h + col
+  uint4 qf[NB][KS];
+  int my_q[NB];                                             // the lane's query position index
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks)
-    qf[ks] = col < n_rows ? *(const uint4*)(Q + qb + (size_t)col * D + 32 * ks + 8 * grp)
-                          : make_uint4(0, 0, 0, 0);
+  for (int h = 0; h < NB; ++h) {
+    const int r = 16 * h + col;
+    my_q[h] = r % g.n_q;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      qf[h][ks] = r < n_rows ? *(const uint4*)(Q + qb + (size_t)r * D + 32 * ks + 8 * grp)
+                             : make_uint4(0, 0, 0, 0);
+  }
   dma_wait();   // the Q loads are complete before any LDS-DMA is in flight
 
   // this lane's chunk of LDS block 4p + wave of a tile: row, swizzled column
@@ -607,11 +614,15 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(
     }
   };
 
-  floatx4 o[DT];
+  floatx4 o[NB][DT];
+  float lsum[NB], m[NB];                       // per column block: row 16h + col
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt) o[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
-  float lsum = 0.f;                            // this lane's 4 tokens per chunk, row col
-  float m = kNegInf;
+  for (int h = 0; h < NB; ++h) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o[h][dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    lsum[h] = 0.f;
+    m[h] = kNegInf;
+  }
 
 #pragma unroll
   for (int c = 0; c < NBUF; ++c)
@@ -623,88 +634,110 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(
     __syncthreads();
     const uint16_t* ck = sk + b * kTileN * D;
     const uint16_t* cv = sv + b * kTileN * D;
-    floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
+    floatx4 s[NB];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) s = T::mfma(lds_row8<D>(ck, 16 * wave + col, 32 * ks + 8 * grp), qf[ks], s);
-    // lane (grp, col): s[i] = score of token t0 + i for q row col
+    for (int h = 0; h < NB; ++h) s[h] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const uint4 a = lds_row8<D>(ck, 16 * wave + col, 32 * ks + 8 * grp);
+#pragma unroll
+      for (int h = 0; h < NB; ++h) s[h] = T::mfma(a, qf[h][ks], s[h]);
+    }
+    // lane (grp, col): s[h][i] = score of token t0 + i for q row 16h + col
     const int t0 = g0 + c * kTileN + 16 * wave + 4 * grp;
+    uint2 pb[NB];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      bool ok = t0 + i < g1;
-      if constexpr (!EXACT)   // several query positions: the token rule per row
-        ok = ok && elem_tok(g, my_q, src.entry(min(t0 + i, g1 - 1)) & kIdxMask);
-      s[i] = ok ? s[i] : kNegInf;
+    for (int h = 0; h < NB; ++h) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        bool ok = t0 + i < g1;
+        if constexpr (!EXACT)   // several query positions: the token rule per row
+          ok = ok && elem_tok(g, my_q[h], src.entry(min(t0 + i, g1 - 1)) & kIdxMask);
+        s[h][i] = ok ? s[h][i] : kNegInf;
+      }
+      float mx = fmaxf(fmaxf(s[h][0], s[h][1]), fmaxf(s[h][2], s[h][3]));
+      if (__any(mx * g.scale_log2 > m[h] + kDecodeSlack)) {
+        mx = wave_max16x4(mx) * g.scale_log2;
+        const bool grow = mx > m[h] + kDecodeSlack;
+        const float alpha = grow ? __builtin_amdgcn_exp2f(m[h] - mx) : 1.f;
+        m[h] = grow ? mx : m[h];
+        lsum[h] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) o[h][dt] *= alpha;
+      }
+      const float m_use = m[h] == kNegInf ? 0.f : m[h];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        s[h][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[h][i], g.scale_log2, -m_use));
+      lsum[h] += (s[h][0] + s[h][1]) + (s[h][2] + s[h][3]);
+      pb[h] = make_uint2(pack2<T>(s[h][0], s[h][1]), pack2<T>(s[h][2], s[h][3]));
     }
-    float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-    if (__any(mx * g.scale_log2 > m + kDecodeSlack)) {
-      mx = wave_max16x4(mx) * g.scale_log2;
-      const bool grow = mx > m + kDecodeSlack;
-      const float alpha = grow ? __builtin_amdgcn_exp2f(m - mx) : 1.f;
-      m = grow ? mx : m;
-      lsum *= alpha;
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+    for (int dt = 0; dt < DT; ++dt) {
+      const uint2 a = lds_tr4<D>(cv, 16 * wave, 16 * dt, lane);
+#pragma unroll
+      for (int h = 0; h < NB; ++h) o[h][dt] = mfma16k<T>(a, pb[h], o[h][dt]);
     }
-    const float m_use = m == kNegInf ? 0.f : m;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) s[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], g.scale_log2, -m_use));
-    lsum += (s[0] + s[1]) + (s[2] + s[3]);
-    const uint2 pb = make_uint2(pack2<T>(s[0], s[1]), pack2<T>(s[2], s[3]));
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) o[dt] = mfma16k<T>(lds_tr4<D>(cv, 16 * wave, 16 * dt, lane), pb, o[dt]);
     __syncthreads();                           // every wave is done with buffer b
     if (c + NBUF < n_chunks) issue(c + NBUF, b);
   }
 
-  // merge the four waves: lane (grp, col) holds O^T rows 16dt + 4grp + i of q row col
-  lsum = wave_sum16x4(lsum);
-  __syncthreads();
+  // merge the four waves, one column block at a time: lane (grp, col) holds
+  // O^T rows 16dt + 4grp + i of q row 16h + col
+  const size_t row_stride = D + 2;
+  float* part = ws + ((size_t)wgh * n_splits + split) * n_rows * row_stride;
   float* wacc = (float*)sk;                    // [4][16][D] (fits two K buffers)
   float* wml = (float*)sv;                     // [4][16][2]
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
+  for (int h = 0; h < NB; ++h) {
+    const float lw = wave_sum16x4(lsum[h]);
+    __syncthreads();                           // the previous block's readers are done
 #pragma unroll
-    for (int i = 0; i < 4; ++i) wacc[(wave * 16 + col) * D + 16 * dt + 4 * grp + i] = o[dt][i];
-  if (grp == 0) {
-    wml[(wave * 16 + col) * 2] = m;
-    wml[(wave * 16 + col) * 2 + 1] = lsum;
-  }
-  __syncthreads();
-  const size_t row_stride = D + 2;
-  float* part = ws + ((size_t)wgh * n_splits + split) * n_rows * row_stride;
-  for (int idx = tid; idx < n_rows * D; idx += 256) {
-    const int r = idx / D, d = idx - r * D;
-    float M = kNegInf;
+    for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-    for (int w = 0; w < 4; ++w) M = fmaxf(M, wml[(w * 16 + r) * 2]);
-    const float Mu = M == kNegInf ? 0.f : M;
-    float L = 0.f, a = 0.f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float sw = __builtin_amdgcn_exp2f(wml[(w * 16 + r) * 2] - Mu);
-      L += wml[(w * 16 + r) * 2 + 1] * sw;
-      a += wacc[(w * 16 + r) * D + d] * sw;
+      for (int i = 0; i < 4; ++i) wacc[(wave * 16 + col) * D + 16 * dt + 4 * grp + i] = o[h][dt][i];
+    if (grp == 0) {
+      wml[(wave * 16 + col) * 2] = m[h];
+      wml[(wave * 16 + col) * 2 + 1] = lw;
     }
-    if (n_splits == 1) {
-      const bool valid = L > 0.f;
-      O[qb + (size_t)r * D + d] = T::from_float(valid ? a / L : 0.f);
-      if (d == 0) LSE[(size_t)bhq0 * g.n_q + r] = valid ? M * kLn2 + __logf(L) : 0.f;
-    } else {
-      part[r * row_stride + d] = a;
-      if (d == 0) {
-        part[r * row_stride + D] = M;
-        part[r * row_stride + D + 1] = L;
+    __syncthreads();
+    const int rows_h = min(16, n_rows - 16 * h);
+    for (int idx = tid; idx < rows_h * D; idx += 256) {
+      const int rl = idx / D, d = idx - rl * D, r = 16 * h + rl;
+      float M = kNegInf;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) M = fmaxf(M, wml[(w * 16 + rl) * 2]);
+      const float Mu = M == kNegInf ? 0.f : M;
+      float L = 0.f, a = 0.f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float sw = __builtin_amdgcn_exp2f(wml[(w * 16 + rl) * 2] - Mu);
+        L += wml[(w * 16 + rl) * 2 + 1] * sw;
+        a += wacc[(w * 16 + rl) * D + d] * sw;
+      }
+      if (n_splits == 1) {
+        const bool valid = L > 0.f;
+        O[qb + (size_t)r * D + d] = T::from_float(valid ? a / L : 0.f);
+        if (d == 0) LSE[(size_t)bhq0 * g.n_q + r] = valid ? M * kLn2 + __logf(L) : 0.f;
+      } else {
+        part[r * row_stride + d] = a;
+        if (d == 0) {
+          part[r * row_stride + D] = M;
+          part[r * row_stride + D + 1] = L;
+        }
       }
     }
   }
 }
 
 // The matrix-core decode serves the group * n_q query rows of a K / V stream
-// when they are 2..kDecodeTileM (16-bit, head_dim 64 / 128), the whole group in
-// one workgroup (one K / V read per group); a single row keeps decode_kernel.
+// when they are 2 .. 2 * kDecodeTileM (16-bit, head_dim 64 / 128; one or two
+// 16-column blocks), the whole group in one workgroup (one K / V read per
+// group); a single row keeps decode_kernel.
 inline bool decode_on_mfma(int dtype, int head_dim, const Geom& g) {
   const int rows = g.group * g.n_q;
-  return dtype != kF32 && (head_dim == 64 || head_dim == 128) && rows >= 2 && rows <= kDecodeTileM;
+  return dtype != kF32 && (head_dim == 64 || head_dim == 128) && rows >= 2 &&
+         rows <= 2 * kDecodeTileM;
 }
 
 template <typename T, int D>
@@ -720,23 +753,28 @@ int launch_decode_mfma(const Geom& g, const void* q, const void* k, const void* 
     if (hipGetDevice(&dev) != hipSuccess) return fail(3, std::string(what) + ": hipGetDevice failed");
     const uint64_t bit = dev < 64 ? (1ull << dev) : 0;
     if (!bit || !(done.load() & bit)) {
-      if (hipFuncSetAttribute((const void*)decode_mfma_kernel<T, D, true>,
+      if (hipFuncSetAttribute((const void*)decode_mfma_kernel<T, D, true, 1>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess ||
-          hipFuncSetAttribute((const void*)decode_mfma_kernel<T, D, false>,
+          hipFuncSetAttribute((const void*)decode_mfma_kernel<T, D, false, 1>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess ||
+          hipFuncSetAttribute((const void*)decode_mfma_kernel<T, D, true, 2>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess ||
+          hipFuncSetAttribute((const void*)decode_mfma_kernel<T, D, false, 2>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
         return fail(3, std::string(what) + ": cannot reserve LDS for the matrix-core decode");
       done.fetch_or(bit);
     }
   }
-  if (g.n_q == 1)
-    hipLaunchKernelGGL((decode_mfma_kernel<T, D, true>), dim3(n_wgh * n_splits), dim3(256), lds, stream,
-                       g, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, lse,
-                       ws, src, kv_rows, n_tokens, n_splits);
-  else
-    hipLaunchKernelGGL((decode_mfma_kernel<T, D, false>), dim3(n_wgh * n_splits), dim3(256), lds, stream,
-                       g, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, lse,
-                       ws, src, kv_rows, n_tokens, n_splits);
   const int n_rows = g.group * g.n_q;
+#define GKI_MFMA_DECODE(EX, NBK)                                                                    hipLaunchKernelGGL((decode_mfma_kernel<T, D, EX, NBK>), dim3(n_wgh * n_splits), dim3(256), lds,                       stream, g, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,                             (uint16_t*)o, lse, ws, src, kv_rows, n_tokens, n_splits)
+  if (n_rows <= kDecodeTileM) {
+    if (g.n_q == 1) GKI_MFMA_DECODE(true, 1);
+    else GKI_MFMA_DECODE(false, 1);
+  } else {
+    if (g.n_q == 1) GKI_MFMA_DECODE(true, 2);
+    else GKI_MFMA_DECODE(false, 2);
+  }
+#undef GKI_MFMA_DECODE
   if (n_splits > 1)
     hipLaunchKernelGGL((combine_kernel<T, D>), dim3(n_wgh * n_rows), dim3(64), 0, stream, ws,
                        (uint16_t*)o, lse, n_rows, n_splits);

@@ -74,10 +74,10 @@ def _decode_splits(n_tokens: int, bh: int) -> int:
 
 def _decode_on_mfma(dtype_code: int, D: int, group: int, n_q: int, max_rows: int) -> bool:
     """The library's ``decode_on_mfma`` rule: a computed-stream decode whose
-    group * n_q query rows per K / V stream are 2 .. ``max_rows``
-    (decode_tile_m), 16-bit, head_dim 64 / 128, runs on the matrix cores, one
-    workgroup per K / V stream (and split)."""
-    return dtype_code != 0 and D in (64, 128) and 2 <= group * n_q <= max_rows
+    group * n_q query rows per K / V stream are 2 .. 2 * ``max_rows``
+    (decode_tile_m: one or two 16-column blocks), 16-bit, head_dim 64 / 128,
+    runs on the matrix cores, one workgroup per K / V stream (and split)."""
+    return dtype_code != 0 and D in (64, 128) and 2 <= group * n_q <= 2 * max_rows
 
 
 def _decode_slots(B: int, H: int, H_kv: int, n_q: int, max_q: int, mfma: bool = False) -> int:

@@ -14,7 +14,8 @@
  *    store (no atomics). The decode kernels serve a group's q heads from one
  *    K / V stream when (H / H_kv) * n_q <= decode_max_q, and, for 16-bit
  *    inputs (head_dim 64 / 128), when the computed-stream decode
- *    (gki_rolling_decode) has 2 .. decode_tile_m query rows per K / V stream.
+ *    (gki_rolling_decode) has 2 .. 2 * decode_tile_m query rows per K / V
+ *    stream.
  *  - dtype codes: 0 = fp32, 1 = fp16, 2 = bf16. head_dim in {16, 32, 64, 128}.
  *  - The block mask is an int32 [n_qb, n_kb] device array with
  *    n_qb = ceil(N_Q / block_m), n_kb = ceil(N_KV / block_n), shared across B, H.

@@ -151,7 +151,9 @@ def test_gqa_prefill_fwd_bwd(B, H, H_kv, n_q, n_kv, D, bm, bn, S, W, dtype):
     (6, 3, 2, 128, torch.bfloat16, 1024),   # 2 heads x 2 rows
     (16, 2, 1, 128, torch.bfloat16, 1024),  # group 8 (matrix cores: 8 of 16 columns)
     (32, 2, 1, 64, torch.float16, 1024),    # group 16: all 16 columns
-    (32, 1, 1, 128, torch.bfloat16, 1024),  # group 32 > 16: one head per workgroup, shared L2
+    (32, 1, 1, 128, torch.bfloat16, 1024),  # group 32: two 16-column blocks
+    (32, 2, 2, 64, torch.float16, 1024),    # 16 heads x 2 positions: two blocks, token rule per row
+    (64, 1, 1, 64, torch.bfloat16, 1024),   # group 64 > 32 rows: one head per workgroup, shared L2
 ])
 def test_gqa_decode_and_rolling_cache(H, H_kv, n_q, D, dtype, W):
     B, n_kv, S = 2, 5000, 4

@@ -122,8 +122,8 @@ def _close(ours, ref, dtype, what):
 
 def _on_matrix_cores(dtype, D, group, n_q):
     """The library's rule for the matrix-core decode of a computed stream
-    (16-bit, head_dim 64 / 128, 2..16 query rows per K / V stream)."""
-    return dtype != torch.float32 and D in (64, 128) and 2 <= group * n_q <= 16
+    (16-bit, head_dim 64 / 128, 2..32 query rows per K / V stream)."""
+    return dtype != torch.float32 and D in (64, 128) and 2 <= group * n_q <= 32
 
 
 def _full_cache_decode(q, k, v, sink, window):
