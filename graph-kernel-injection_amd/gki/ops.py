@@ -225,8 +225,8 @@ class _BlockSparseFlashAttention(torch.autograd.Function):
         dk = torch.empty_like(k)
         dv = torch.empty_like(v)
         delta = torch.empty((B, H, N_Q), dtype=torch.float32, device=q.device)
-        with torch.cuda.device(q.device):
-            stream = torch.cuda.current_stream(q.device).cuda_stream
+        with _on_device(q.device):
+            stream = _current_stream(q.device)
             sched = bwd_schedule(block_mask, N_Q, N_KV, ctx.block_m, ctx.block_n, ctx.is_causal,
                                  ctx.sink_size, ctx.window_size, group=H // H_kv, bh_kv=B * H_kv)
             L = sched.lists
