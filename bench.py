@@ -263,34 +263,38 @@ def section_c4(steps: int, warmup: int) -> dict:
     res["rolling_cache"] = _rolling_c4(q, k, v, S, W, fn(), exact_bytes, steps, warmup)
     del k, v
     res["gqa"] = _gqa_c4(B, H, NKV, D, S, W, mask, steps, warmup)
+    res["multi_query"] = _gqa_c4(B, H, NKV, D, S, W, mask, steps, warmup, H_kv=1)
+    res["four_positions"] = _gqa_c4(B, H, NKV, D, S, W, mask, steps, warmup, H_kv=H, n_q=4)
     return res
 
 
-def _gqa_c4(B, H, NKV, D, S, W, mask, steps, warmup) -> dict:
-    """The c4 step with grouped-query K/V (8 kv heads for the 32 q heads): each
-    decode workgroup serves a group's 4 q heads from one K/V stream, so the
-    token-exact K/V bytes are a quarter of c4's."""
+def _gqa_c4(B, H, NKV, D, S, W, mask, steps, warmup, H_kv=8, n_q=1) -> dict:
+    """The c4 step with grouped-query K/V (default: 8 kv heads for the 32 q
+    heads) and / or n_q query positions: a K/V stream's group x n_q query rows
+    are served by one workgroup (on the matrix cores for 2..32 rows), so the
+    token-exact K/V bytes are H_kv / H of c4's (positions visible to any row)."""
     import torch
 
     import sparse_triton_kernel as stk
 
-    H_kv = 8
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(5)
-    q = torch.randn(B, H, 1, D, generator=g, device=dev).to(torch.bfloat16)
+    q = torch.randn(B, H, n_q, D, generator=g, device=dev).to(torch.bfloat16)
     k = torch.randn(B, H_kv, NKV, D, generator=g, device=dev).to(torch.bfloat16)
     v = torch.randn(B, H_kv, NKV, D, generator=g, device=dev).to(torch.bfloat16)
+    if n_q != 1:
+        mask = stk.make_streaming_mask(n_q, NKV, stk.StreamingMaskSpec(S, W), 1, 64, device=dev)
 
     def fn():
         return stk.block_sparse_attention(q, k, v, mask, block_m=1, block_n=64, is_causal=True,
-                                          sink_size=S, window_size=W, enable_gqa=True)
+                                          sink_size=S, window_size=W, enable_gqa=H_kv != H)
 
     avg, per = _time_calls(fn, steps, warmup)
-    kv_bytes = (S + W) * D * 2 * 2 * B * H_kv
+    kv_bytes = (S + W + n_q - 1) * D * 2 * 2 * B * H_kv
     gbs = kv_bytes / (avg * 1e-3) / 1e9
-    log(f"[c4] GQA H{H}/H_kv{H_kv}: decode step {avg * 1e3:.2f} us, {gbs:.0f} GB/s token-exact "
+    log(f"[c4] H{H}/H_kv{H_kv} n_q {n_q}: decode step {avg * 1e3:.2f} us, {gbs:.0f} GB/s token-exact "
         f"({kv_bytes / 1e6:.0f} MB of K/V)")
-    return {"workload": f"c4 with grouped-query K/V: H {H}, H_kv {H_kv}", "kv_bytes_token_exact": kv_bytes,
+    return {"workload": f"c4 with H {H}, H_kv {H_kv}, n_q {n_q}", "kv_bytes_token_exact": kv_bytes,
             "avg_ms": avg, "p50_ms": statistics.median(per), "kv_gbs": gbs}
 
 

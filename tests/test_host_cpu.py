@@ -121,6 +121,30 @@ def test_dkdv_work_list_matches_oracle():
         np.testing.assert_array_equal(split.numpy()[:n_split], want_split)
 
 
+def test_decode_routing_rules():
+    """The op's decode plan mirrors the library: 2..32 query rows per K / V
+    stream of a 16-bit computed-stream step run on the matrix cores with one
+    slot per stream; otherwise a group shares a workgroup only within the 4-row
+    kernel's limit."""
+    from gki import ops
+
+    tile_m = 16
+    assert ops._decode_on_mfma(2, 128, 4, 1, tile_m)            # grouped-query, one position
+    assert ops._decode_on_mfma(1, 64, 1, 4, tile_m)             # multi-head, 4 positions
+    assert ops._decode_on_mfma(2, 128, 32, 1, tile_m)           # 32 rows: two column blocks
+    assert not ops._decode_on_mfma(2, 128, 1, 1, tile_m)        # one row: the vector kernel
+    assert not ops._decode_on_mfma(2, 128, 64, 1, tile_m)       # 64 rows
+    assert not ops._decode_on_mfma(0, 128, 4, 1, tile_m)        # fp32
+    assert not ops._decode_on_mfma(2, 32, 4, 1, tile_m)         # head_dim 32
+    assert ops._decode_slots(8, 32, 8, 1, 4, mfma=True) == 64
+    assert ops._decode_slots(8, 32, 8, 1, 4) == 64              # group 4 fits the 4-row kernel
+    assert ops._decode_slots(8, 32, 2, 1, 4) == 256             # group 16: one q head each
+    assert ops._decode_slots(8, 32, 32, 2, 4) == 256
+    # about one workgroup per CU, at least ~256 tokens each
+    assert ops._decode_splits(2052, 64) == 4 and ops._decode_splits(2052, 256) == 1
+    assert ops._decode_splits(2052, 8) == 8 and ops._decode_splits(100, 1) == 1
+
+
 def test_dkdv_work_list_rejects_bad_columns():
     lib = _lib.load()
     out = [ctypes.c_int32() for _ in range(3)]
