@@ -14,8 +14,10 @@ KV GB/s, each as a fraction of the MI355X roofline.
 * ``layer_c5`` -- one config-5 attention layer (1x16x131072x64 bf16, S4 W4096,
   128x64 blocks), fwd + bwd.
 * ``cpu_baseline`` -- the reference's eager masked attention (restated in
-  ``oracle/eager_cpu.py``) in fp32 on the host cores, on a bounded sample of
-  config 2 (whole heads until ~10 s of CPU time), in the same unit.
+  ``oracle/eager_cpu.py``) in fp32 on the host cores (thread count and CPU
+  model recorded), on bounded samples of the same inputs: config 2 forward
+  (``value``, same unit as the headline), config 3 forward + backward and
+  config 4 decode (whole (b, h) slices until each leg's share of ~24 s).
 
 Inputs are synthetic N(0, 1) (config 2 scaled by 0.5), generated once and
 resident in HBM before the timed region. Each section first runs its step
@@ -34,6 +36,7 @@ import statistics
 import sys
 import time
 from pathlib import Path
+from typing import Optional
 
 ROOT = Path(__file__).resolve().parent
 for _p in (ROOT / "graph-kernel-injection_amd", ROOT):
@@ -173,7 +176,7 @@ def section_c2(steps: int, warmup: int, keep_cpu_inputs: bool):
     }, cpu_inputs
 
 
-def section_c3(steps: int, warmup: int) -> dict:
+def section_c3(steps: int, warmup: int, cpu_sample: Optional[dict] = None) -> dict:
     import torch
 
     import sparse_triton_kernel as stk
@@ -219,10 +222,12 @@ def section_c3(steps: int, warmup: int) -> dict:
                                 _traffic("c3_fwd", "c3_dkdv", "c3_dq"))
     log(f"[c3] fwd {fwd:.4f} ms ({res['fwd_tflops']:.1f} TF/s), bwd {bwd:.4f} ms "
         f"({res['bwd_tflops']:.1f} TF/s)")
+    if cpu_sample is not None:
+        cpu_sample["c3"] = tuple(t.detach().cpu() for t in (q, k, v, do)) + (mask.cpu(), kept)
     return res
 
 
-def section_c4(steps: int, warmup: int) -> dict:
+def section_c4(steps: int, warmup: int, cpu_sample: Optional[dict] = None) -> dict:
     import torch
 
     import sparse_triton_kernel as stk
@@ -236,7 +241,7 @@ def section_c4(steps: int, warmup: int) -> dict:
     mask = stk.make_streaming_mask(1, NKV, stk.StreamingMaskSpec(S, W), 1, 64, device=dev)
     kept = int(mask.sum().item())
     exact_bytes = (S + W) * D * 2 * 2 * B * H
-    block_bytes = kept * 64 * D * 2 * 2 * B * H
+    block_bytes = block_granular_tokens(mask[0].cpu(), NKV, 64) * D * 2 * 2 * B * H
 
     def fn():
         return stk.block_sparse_attention(q, k, v, mask, block_m=1, block_n=64, is_causal=True,
@@ -261,6 +266,8 @@ def section_c4(steps: int, warmup: int) -> dict:
     log(f"[c4] decode step after evicting the memory-side cache: {cold * 1e3:.2f} us, "
         f"{res['cold_cache']['kv_gbs']:.0f} GB/s ({100 * res['cold_cache']['frac']:.1f}% of HBM peak)")
     res["rolling_cache"] = _rolling_c4(q, k, v, S, W, fn(), exact_bytes, steps, warmup)
+    if cpu_sample is not None:      # batch 0's 32 heads: (b, h) slices for the CPU leg
+        cpu_sample["c4"] = (q[:1].cpu(), k[:1].cpu(), v[:1].cpu(), mask.cpu())
     del k, v
     res["gqa"] = _gqa_c4(B, H, NKV, D, S, W, mask, steps, warmup)
     res["multi_query"] = _gqa_c4(B, H, NKV, D, S, W, mask, steps, warmup, H_kv=1)
@@ -374,32 +381,120 @@ def section_c5(steps: int, warmup: int) -> dict:
     return res
 
 
-def cpu_baseline(cpu_inputs, kept: int, budget_s: float) -> dict:
-    """Reference eager path (fp32, all host threads) on whole heads of config 2."""
+def block_granular_tokens(kept_row, n_kv: int, bn: int) -> int:
+    """In-bounds tokens of the kept tiles of a one-row block mask: bn per kept
+    tile, the ragged last tile only its n_kv - bn * j in-range tokens (c4: 33
+    full tiles + 32 tokens of tile 1562 = 2144 tokens)."""
+    cols = [j for j, x in enumerate(kept_row.tolist()) if x]
+    return sum(min(bn, n_kv - bn * j) for j in cols)
+
+
+def cpu_threads() -> int:
+    """Host threads for the CPU baseline: the cores this process may run on,
+    capped by OMP_NUM_THREADS when the environment sets it (the GPU box
+    allots each GPU a share of its cores and says so there)."""
+    n = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return max(1, n)
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _heads_within(budget_s: float, n_heads: int, one_head) -> tuple:
+    """Run one_head(i) for i = 0, 1, ... until the budget is spent (at least
+    once, at most n_heads times); returns (heads done, seconds)."""
+    heads = 0
+    t0 = time.perf_counter()
+    while heads < n_heads:
+        one_head(heads)
+        heads += 1
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    return heads, time.perf_counter() - t0
+
+
+def cpu_baseline(cpu_inputs, kept: int, budget_s: float, extra: Optional[dict] = None) -> dict:
+    """The reference's eager path (sparse_triton_kernel.py:845-902, restated in
+    oracle/eager_cpu.py) in fp32 on the host cores, on bounded samples of the
+    same inputs the GPU sections used (whole (b, h) slices until each leg's
+    share of the budget is spent; sums over slices, extrapolation stated):
+    config 2 forward (``value``, kept-block TFLOP/s), and from ``extra``
+    config 3 forward + backward (autograd; 14 * BM * BN * D per kept tile)
+    and config 4 decode steps (token-exact kept K/V GB/s)."""
     import torch
 
     from oracle.eager_cpu import eager_masked_attention
 
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    extra = extra or {}
+    legs = 1 + ("c3" in extra) + ("c4" in extra)
+    share = budget_s / legs
+
     q, k, v, mask = cpu_inputs
     H, D = q.shape[1], q.shape[-1]
-    threads = torch.get_num_threads()
-    heads = 0
-    t0 = time.perf_counter()
-    while heads < H:
-        sl = slice(heads, heads + 1)
+
+    def c2_head(h):
+        sl = slice(h, h + 1)
         eager_masked_attention(q[:, sl], k[:, sl], v[:, sl], mask, 64, 64, True, 4, 2048)
-        heads += 1
-        if time.perf_counter() - t0 >= budget_s:
-            break
-    elapsed = time.perf_counter() - t0
-    flops = 4.0 * 64 * 64 * D * kept * heads
-    tflops = flops / elapsed / 1e12
-    log(f"[cpu] eager fp32 on {threads} threads: {heads} head(s) in {elapsed:.1f} s, "
+
+    heads, elapsed = _heads_within(share, H, c2_head)
+    tflops = 4.0 * 64 * 64 * D * kept * heads / elapsed / 1e12
+    log(f"[cpu] eager fp32 on {threads} threads: c2 {heads} head(s) in {elapsed:.1f} s, "
         f"{tflops * 1e3:.2f} GFLOP/s kept-block")
-    return {"value": round(tflops, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": (f"config 2 forward, {heads} of {H} heads (B1 N16384 D128, fp32 eager "
-                       f"masked attention over all keys, 2048-row chunks), {elapsed:.1f} s; "
-                       f"full-step extrapolation {elapsed * H / heads:.1f} s")}
+    out = {"value": round(tflops, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+           "cpu_model": cpu_model(), "os_cpu_count": os.cpu_count(),
+           "sample": (f"config 2 forward, {heads} of {H} heads (B1 N16384 D128, fp32 eager "
+                      f"masked attention over all keys, 2048-row chunks), {elapsed:.1f} s; "
+                      f"full-step extrapolation {elapsed * H / heads:.1f} s")}
+
+    if "c3" in extra:
+        q3, k3, v3, do3, m3, kept3 = extra["c3"]
+        B3, H3, N3, D3 = q3.shape
+
+        def c3_head(i):
+            b, h = divmod(i, H3)
+            sl = (slice(b, b + 1), slice(h, h + 1))
+            leaves = [t[sl].float().requires_grad_(True) for t in (q3, k3, v3)]
+            o = eager_masked_attention(*leaves, m3, 64, 64, True, 4, 1024)
+            o.backward(do3[sl].float())
+
+        n3, t3 = _heads_within(share, B3 * H3, c3_head)
+        f3 = 14.0 * 64 * 64 * D3 * kept3 * n3
+        out["c3"] = {"value": round(f3 / t3 / 1e12, 6), "unit": "TFLOP/s",
+                     "sample": (f"config 3 forward + backward (autograd), {n3} of {B3 * H3} (b, h) "
+                                f"slices (N8192 D64), {t3:.1f} s; full-step extrapolation "
+                                f"{t3 * B3 * H3 / n3:.1f} s")}
+        log(f"[cpu] c3 fwd+bwd: {n3} (b, h) slice(s) in {t3:.1f} s, "
+            f"{out['c3']['value'] * 1e3:.2f} GFLOP/s kept-block")
+
+    if "c4" in extra:
+        q4, k4, v4, m4 = extra["c4"]
+        H4, N4, D4 = q4.shape[1], k4.shape[2], q4.shape[-1]
+
+        def c4_head(h):
+            sl = (slice(0, 1), slice(h, h + 1))
+            eager_masked_attention(q4[sl].float(), k4[sl].float(), v4[sl].float(), m4, 1, 64, True,
+                                   4, 2048)
+
+        n4, t4 = _heads_within(share, H4, c4_head)
+        kv = (4 + 2048) * D4 * 2 * 2 * n4
+        out["c4"] = {"value": round(kv / t4 / 1e9, 4), "unit": "GB/s",
+                     "sample": (f"config 4 decode, {n4} of 256 (b, h) slices (n_q 1, KV 100000, "
+                                f"D128; the eager path reads all 100000 keys), {t4:.2f} s; "
+                                f"token-exact kept K/V bytes {kv} over that time")}
+        log(f"[cpu] c4 decode: {n4} (b, h) slice(s) in {t4:.2f} s, {out['c4']['value']:.3f} GB/s")
+    return out
 
 
 def copy_calibration() -> None:
@@ -423,7 +518,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--sections", default="c2,c3,c4,c5,cpu",
                     help="comma list among c2,c3,c4,c5,cpu (c2 is always run)")
-    ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline work")
+    ap.add_argument("--cpu-budget", type=float, default=24.0,
+                    help="seconds of CPU baseline work, shared by its c2 / c3 / c4 legs")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (counter calibration), print nothing on stdout")
     args = ap.parse_args()
@@ -463,18 +559,19 @@ def main() -> int:
         "roofline": _roofline(c2["tflops"], PEAK_MFMA_16, "TFLOP/s", "mfma", _traffic("c2_fwd")),
     }
     torch.cuda.empty_cache()
+    cpu_extra = {} if "cpu" in sections else None
     if "c3" in sections:
-        line["train"] = section_c3(args.steps, args.warmup)
+        line["train"] = section_c3(args.steps, args.warmup, cpu_extra)
         torch.cuda.empty_cache()
     if "c4" in sections:
         # a decode step is ~45 us: time more of them for a stable mean
-        line["decode"] = section_c4(max(args.steps, 200), max(args.warmup, 20))
+        line["decode"] = section_c4(max(args.steps, 200), max(args.warmup, 20), cpu_extra)
         torch.cuda.empty_cache()
     if "c5" in sections:
         line["layer_c5"] = section_c5(max(3, args.steps // 4), 2)
         torch.cuda.empty_cache()
     if "cpu" in sections:
-        line["cpu_baseline"] = cpu_baseline(cpu_in, c2["kept_tiles"], args.cpu_budget)
+        line["cpu_baseline"] = cpu_baseline(cpu_in, c2["kept_tiles"], args.cpu_budget, cpu_extra)
     print(json.dumps(line), flush=True)
     return 0
 

@@ -8,7 +8,8 @@
 //       for dK/dV; for fp32 inputs delta_kernel, before the other two.
 //   * dkdv_kernel   <- `_bwd_dkdv_kernel` (sparse_triton_kernel.py:394-509):
 //       one workgroup per 64-row KV tile, loop over the kept q tiles of its
-//       column (CSC list), P = exp(S - LSE), dV += P^T dO, dS = P (dP - Delta)
+//       column (CSC list), P = exp(S - LSE) (as exp2 of base-2 terms; the
+//       forward stores the LSE in base 2), dV += P^T dO, dS = P (dP - Delta)
 //       * scale, dK += dS^T Q. No atomics; one store per tile.
 //   * dq_kernel     <- `_bwd_dq_kernel` (sparse_triton_kernel.py:511-601):
 //       one workgroup per 64-row q tile, loop over its kept kv tiles (CSR),
@@ -58,6 +59,22 @@ __global__ __launch_bounds__(256) void delta_kernel(const typename T::storage* _
 #pragma unroll
   for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
   if (row < rows && ch == 0) delta[row] = acc;
+}
+
+// fp32 gradients accumulate one iteration (64 rows) at a time in a fresh
+// accumulator, which is then added to the running sum with its rounding error
+// kept exactly (TwoSum) in a compensation term: a long walk (the sink keys of a
+// long sequence, |dV| ~ 10 over thousands of rows) then rounds like a short
+// one. The result is sum + compensation.
+__device__ inline void two_sum_fold(floatx4& sum, floatx4& comp, const floatx4& x) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float s = sum[i] + x[i];
+    const float bp = s - sum[i];
+    const float ap = s - bp;
+    comp[i] += (sum[i] - ap) + (x[i] - bp);
+    sum[i] = s;
+  }
 }
 
 template <int D>
@@ -122,6 +139,16 @@ __global__ __launch_bounds__(256) void dkdv_reduce_kernel(Geom g, KvWork w,
   const float4* src = (const float4*)(w.partials + ((size_t)bh * w.n_pslots + p0) * 2 * TILE + idx);
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
   int c = 0;
+  if constexpr (T::is_f32) {           // compensated (Kahan) sum of the fp32 partials
+    float4 comp = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (; c < np; ++c) {
+      const float4 a = src[(size_t)c * STRIDE];
+      const float ya = a.x - comp.x, yb = a.y - comp.y, yc = a.z - comp.z, yd = a.w - comp.w;
+      const float ta = acc.x + ya, tb = acc.y + yb, tc = acc.z + yc, td = acc.w + yd;
+      comp = make_float4((ta - acc.x) - ya, (tb - acc.y) - yb, (tc - acc.z) - yc, (td - acc.w) - yd);
+      acc = make_float4(ta, tb, tc, td);
+    }
+  }
   for (; c + 4 <= np; c += 4) {
     const float4 a0 = src[(size_t)c * STRIDE], a1 = src[(size_t)(c + 1) * STRIDE];
     const float4 a2 = src[(size_t)(c + 2) * STRIDE], a3 = src[(size_t)(c + 3) * STRIDE];
@@ -258,7 +285,7 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
       const int qr0 = rho(t, 4 * grp);
       const float4 lse4 = *(const float4*)(&slse[buf][qr0]);
       const float4 dlt4 = *(const float4*)(&sdlt[buf][qr0]);
-      const float lv[4] = {lse4.x * kLog2e, lse4.y * kLog2e, lse4.z * kLog2e, lse4.w * kLog2e};
+      const float lv[4] = {lse4.x, lse4.y, lse4.z, lse4.w};          // base-2 LSE
       const float dv4[4] = {dlt4.x, dlt4.y, dlt4.z, dlt4.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -334,7 +361,7 @@ struct DkdvSmem32 {
 };
 
 template <int D>
-__global__ __launch_bounds__(256, 2) void dkdv_kernel_32(
+__global__ __launch_bounds__(256, D >= 128 ? 1 : 2) void dkdv_kernel_32(
     Geom g, const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ dO, float* __restrict__ dK, float* __restrict__ dV,
     const float* __restrict__ LSE, const float* __restrict__ Delta,
@@ -364,9 +391,9 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_32(
     kf[ks] = ok ? K[kb + (size_t)my_kv * D + 4 * ks + grp] : 0.f;
     vf[ks] = ok ? V[kb + (size_t)my_kv * D + 4 * ks + grp] : 0.f;
   }
-  floatx4 dk[DT], dv[DT];
+  floatx4 dk[DT], dv[DT], ck[DT], cv[DT];   // running sums and their compensation
 #pragma unroll
-  for (int i = 0; i < DT; ++i) dk[i] = dv[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < DT; ++i) dk[i] = dv[i] = ck[i] = cv[i] = floatx4{0.f, 0.f, 0.f, 0.f};
 
   const int e_beg = col_ptr[kt], e_end = col_ptr[kt + 1];
   float lreg = 0.f, dreg = 0.f;
@@ -376,7 +403,7 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_32(
     sdo.load(dO + qb, q0, g.n_q, tid);
     if (tid < 64) {
       const int r = q0 + tid;
-      lreg = r < g.n_q ? LSE[(size_t)bhq * g.n_q + r] * kLog2e : 0.f;
+      lreg = r < g.n_q ? LSE[(size_t)bhq * g.n_q + r] : 0.f;   // base 2
       dreg = r < g.n_q ? Delta[(size_t)bhq * g.n_q + r] : 0.f;
     }
   };
@@ -407,16 +434,16 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_32(
 
     const bool need_mask = partial || (q0 + kTileM > g.n_q) || (k_w + 15 >= g.n_kv) ||
                            !tile_all_visible(g, q0, min(q0 + kTileM - 1, g.n_q - 1), k_w, kv_hi_wave);
+    floatx4 fk[DT], fv[DT];            // this iteration's 64 rows
+#pragma unroll
+    for (int i = 0; i < DT; ++i) fk[i] = fv[i] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
-      floatx4 dp = floatx4{0.f, 0.f, 0.f, 0.f};
       const int r = rho(t, col);
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        s = mfma_f32(sm.q[r * LD + 4 * ks + grp], kf[ks], s);
-        dp = mfma_f32(sm.dout[r * LD + 4 * ks + grp], vf[ks], dp);
-      }
+      const floatx4 s = mfma_f32_dot<KS>([&](int ks) { return sm.q[r * LD + 4 * ks + grp]; },
+                                         [&](int ks) { return kf[ks]; });
+      const floatx4 dp = mfma_f32_dot<KS>([&](int ks) { return sm.dout[r * LD + 4 * ks + grp]; },
+                                          [&](int ks) { return vf[ks]; });
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int qr = rho(t, 4 * grp + i);
@@ -425,11 +452,21 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_32(
         const float dsv = pv * (dp[i] - sm.dlt[qr]) * g.scale;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-          dv[dt] = mfma_f32(pv, sm.dout[qr * LD + 16 * dt + col], dv[dt]);
-          dk[dt] = mfma_f32(dsv, sm.q[qr * LD + 16 * dt + col], dk[dt]);
+          fv[dt] = mfma_f32(pv, sm.dout[qr * LD + 16 * dt + col], fv[dt]);
+          fk[dt] = mfma_f32(dsv, sm.q[qr * LD + 16 * dt + col], fk[dt]);
         }
       }
     }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      two_sum_fold(dk[dt], ck[dt], fk[dt]);
+      two_sum_fold(dv[dt], cv[dt], fv[dt]);
+    }
+  }
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    dk[dt] += ck[dt];
+    dv[dt] += cv[dt];
   }
   if (item.pslot >= 0) {             // a split column: partials for the reduce
     float* pk = w.partials + ((size_t)bh * w.n_pslots + item.pslot) * 2 * (kTileN * D);
@@ -493,7 +530,7 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_16(
     qf[ks] = ok ? *(const uint4*)(Q + qb + (size_t)my_q * D + d0) : make_uint4(0, 0, 0, 0);
     df[ks] = ok ? *(const uint4*)(dO + qb + (size_t)my_q * D + d0) : make_uint4(0, 0, 0, 0);
   }
-  const float lse2 = my_q < g.n_q ? LSE[(size_t)bh * g.n_q + my_q] * kLog2e : 0.f;
+  const float lse2 = my_q < g.n_q ? LSE[(size_t)bh * g.n_q + my_q] : 0.f;   // base 2
   // Delta = rowsum(O * dO) in fp32 over the stored O (the preprocessing pass,
   // sparse_triton_kernel.py:354-392, fused here): the lane already holds its
   // row's dO chunks, the four lane groups of a row are summed across. Every q
@@ -637,11 +674,11 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_32(
     qf[ks] = ok ? Q[qb + (size_t)my_q * D + 4 * ks + grp] : 0.f;
     df[ks] = ok ? dO[qb + (size_t)my_q * D + 4 * ks + grp] : 0.f;
   }
-  const float lse2 = my_q < g.n_q ? LSE[(size_t)bh * g.n_q + my_q] * kLog2e : 0.f;
+  const float lse2 = my_q < g.n_q ? LSE[(size_t)bh * g.n_q + my_q] : 0.f;   // base 2
   const float dlt = my_q < g.n_q ? Delta[(size_t)bh * g.n_q + my_q] : 0.f;
-  floatx4 dq[DT];
+  floatx4 dq[DT], cq[DT];              // running sum and its compensation (two_sum_fold)
 #pragma unroll
-  for (int i = 0; i < DT; ++i) dq[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < DT; ++i) dq[i] = cq[i] = floatx4{0.f, 0.f, 0.f, 0.f};
 
   const int e_beg = row_ptr[qt], e_end = row_ptr[qt + 1];
   if (e_beg < e_end) {
@@ -665,16 +702,16 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_32(
     }
     const bool need_mask = partial || (q0 + 15 >= g.n_q) || (k0 + kTileN > g.n_kv) ||
                            !tile_all_visible(g, q0, q_hi_wave, k0, k0 + kTileN - 1);
+    floatx4 fq[DT];                    // this iteration's 64 keys
+#pragma unroll
+    for (int i = 0; i < DT; ++i) fq[i] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
-      floatx4 dp = floatx4{0.f, 0.f, 0.f, 0.f};
       const int r = rho(t, col);
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        s = mfma_f32(sm.k[r * LD + 4 * ks + grp], qf[ks], s);
-        dp = mfma_f32(sm.v[r * LD + 4 * ks + grp], df[ks], dp);
-      }
+      const floatx4 s = mfma_f32_dot<KS>([&](int ks) { return sm.k[r * LD + 4 * ks + grp]; },
+                                         [&](int ks) { return qf[ks]; });
+      const floatx4 dp = mfma_f32_dot<KS>([&](int ks) { return sm.v[r * LD + 4 * ks + grp]; },
+                                          [&](int ks) { return df[ks]; });
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int kr = rho(t, 4 * grp + i);
@@ -682,10 +719,14 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_32(
         if (need_mask && !elem_valid(g, my_q, k0 + kr, partial)) pv = 0.f;
         const float dsv = pv * (dp[i] - dlt) * g.scale;
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) dq[dt] = mfma_f32(sm.k[kr * LD + 16 * dt + col], dsv, dq[dt]);
+        for (int dt = 0; dt < DT; ++dt) fq[dt] = mfma_f32(sm.k[kr * LD + 16 * dt + col], dsv, fq[dt]);
       }
     }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) two_sum_fold(dq[dt], cq[dt], fq[dt]);
   }
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) dq[dt] += cq[dt];
   if (my_q < g.n_q) {
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {

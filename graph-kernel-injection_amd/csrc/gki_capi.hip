@@ -5,7 +5,9 @@
 // message is available from gki_last_error() (thread-local). The library never
 // allocates or frees device memory and keeps no pointer after returning.
 #include <algorithm>
+#include <cmath>
 
+#include "gki_bsa.h"
 #include "gki_common.cuh"
 
 namespace gki {
@@ -55,6 +57,19 @@ namespace {
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 template <typename... P> inline bool all_aligned16(P... p) { return (aligned16(p) && ...); }
 
+// Softmax scale of any finite sign: the signed scale for the kernels that
+// scale each score before the max, and the Q transform plus positive scale
+// for the kernels that take the max on unscaled scores (Geom::q_and). The
+// words are 32-bit: two 16-bit Q elements or one fp32 element (the fp32
+// kernels scale before the max and ignore them).
+void set_scale(Geom& g, float scale) {
+  g.scale = scale;
+  g.scale_log2 = scale * kLog2e;
+  g.q_and = scale == 0.f ? 0u : 0xFFFFFFFFu;
+  g.q_xor = scale < 0.f ? 0x80008000u : 0u;
+  g.qk_scale_log2 = scale == 0.f ? kLog2e : (scale < 0.f ? -scale : scale) * kLog2e;
+}
+
 int make_geom(Geom& g, int dtype, int B, int H, int H_kv, int n_q, int n_kv, int head_dim,
               const int32_t* mask, int n_qb, int n_kb, int block_m, int block_n, float scale, int causal,
               int sink, int window) {
@@ -70,7 +85,7 @@ int make_geom(Geom& g, int dtype, int B, int H, int H_kv, int n_q, int n_kv, int
   GKI_REQUIRE(n_qb == (n_q + block_m - 1) / block_m && n_kb == (n_kv + block_n - 1) / block_n, 1,
               "block mask shape does not match ceil(n_q/block_m) x ceil(n_kv/block_n)");
   GKI_REQUIRE(sink >= 0 && window >= 0, 1, "sink_size and window_size must be non-negative");
-  GKI_REQUIRE(scale > 0.f && scale < __builtin_huge_valf(), 1, "softmax_scale must be positive and finite");
+  GKI_REQUIRE(std::isfinite(scale), 1, "softmax_scale must be finite");
   GKI_REQUIRE((int64_t)n_kv < (1ll << kPartialBit), 1, "n_kv too large");
   GKI_REQUIRE(mask != nullptr, 1, "null block mask");
   g.B = B;
@@ -80,8 +95,7 @@ int make_geom(Geom& g, int dtype, int B, int H, int H_kv, int n_q, int n_kv, int
   g.n_q = n_q;
   g.n_kv = n_kv;
   g.q_off = n_kv - n_q;
-  g.scale = scale;
-  g.scale_log2 = scale * kLog2e;
+  set_scale(g, scale);
   g.causal = causal ? 1 : 0;
   g.sink = sink;
   g.window = window;
@@ -93,6 +107,53 @@ int make_geom(Geom& g, int dtype, int B, int H, int H_kv, int n_q, int n_kv, int
   return 0;
 }
 
+// Argument checks of the rolling-cache decode entry points.
+int rolling_decode_args(int dtype, int B, int H, int H_kv, int n_q, int head_dim, int sink_size,
+                        int window_size, int ring_size, int64_t length, float softmax_scale,
+                        const void* q, const void* k_cache, const void* v_cache, void* o, float* lse,
+                        int n_splits) {
+  GKI_REQUIRE(dtype == kF32 || dtype == kF16 || dtype == kBF16, 2,
+              "unsupported dtype code " + std::to_string(dtype) + " (0=fp32, 1=fp16, 2=bf16)");
+  GKI_REQUIRE(head_dim == 64 || head_dim == 128, 2,
+              "gki_rolling_decode: head_dim must be 64 or 128, got " + std::to_string(head_dim));
+  GKI_REQUIRE(B > 0 && H > 0 && (int64_t)B * H < (1ll << 31) / 4096, 1,
+              "gki_rolling_decode: B and H must be positive and B * H not too large");
+  GKI_REQUIRE(H_kv > 0 && H % H_kv == 0, 1,
+              "H_kv must be positive and divide H (grouped-query attention)");
+  if (int rc = gki_rolling_stream(length, n_q, sink_size, window_size, ring_size, nullptr, nullptr,
+                                  nullptr))
+    return rc;
+  GKI_REQUIRE(std::isfinite(softmax_scale), 1, "softmax_scale must be finite");
+  GKI_REQUIRE(q && k_cache && v_cache && o && lse, 1, "gki_rolling_decode: null pointer");
+  GKI_REQUIRE(all_aligned16(q, k_cache, v_cache), 1, "gki_rolling_decode: q and caches must be 16-byte aligned");
+  GKI_REQUIRE(n_splits >= 1 && (int64_t)n_splits * B * H < (1ll << 31), 1,
+              "gki_rolling_decode: n_splits must be >= 1 and the grid must fit");
+  return 0;
+}
+
+int rolling_decode_checked(const void* q, const void* k_cache, const void* v_cache, void* o, float* lse,
+                           int dtype, int B, int H, int H_kv, int n_q, int head_dim, int sink_size,
+                           int window_size, int ring_size, int64_t length, float softmax_scale,
+                           float* workspace, int n_splits, void* stream) {
+  GKI_REQUIRE(n_splits == 1 || workspace, 1, "gki_rolling_decode: null workspace");
+  Geom g{};
+  g.B = B;
+  g.H = H;
+  g.H_kv = H_kv;
+  g.group = H / H_kv;
+  g.n_q = n_q;
+  g.n_kv = (int)length;                 // positions 0 .. length-1; queries are the last n_q
+  g.q_off = (int)length - n_q;
+  set_scale(g, softmax_scale);
+  g.causal = 1;
+  g.sink = sink_size;
+  g.window = window_size;
+  g.mask = nullptr;                     // no stream entry carries the partial flag
+  g.n_qb = g.n_kb = g.bm = g.bn = 1;
+  return decode_ring_dispatch(dtype, head_dim, g, q, k_cache, v_cache, o, lse, ring_size, workspace,
+                              n_splits, (hipStream_t)stream);
+}
+
 }  // namespace
 }  // namespace gki
 
@@ -100,7 +161,7 @@ using namespace gki;
 
 extern "C" {
 
-int gki_abi_version(void) { return 3; }
+int gki_abi_version(void) { return 4; }
 
 const char* gki_last_error(void) { return g_last_error.c_str(); }
 
@@ -164,8 +225,8 @@ int gki_bsa_bwd(const void* q, const void* k, const void* v, const void* o, cons
 }
 
 int gki_dkdv_items(const int32_t* col_ptr, int32_t n_kt, int32_t group, int32_t bh_kv,
-                   int32_t* items, int32_t* n_items, int32_t* split, int32_t* n_split,
-                   int32_t* n_pslots) {
+                   int32_t max_chunk, int32_t* items, int32_t* n_items, int32_t* split,
+                   int32_t* n_split, int32_t* n_pslots) {
   GKI_REQUIRE(col_ptr && n_items && n_split && n_pslots, 1, "gki_dkdv_items: null pointer");
   GKI_REQUIRE(n_kt >= 1 && group >= 1 && bh_kv >= 1, 1,
               "gki_dkdv_items: n_kt, group and bh_kv must be positive");
@@ -177,8 +238,10 @@ int gki_dkdv_items(const int32_t* col_ptr, int32_t n_kt, int32_t group, int32_t 
   }
   total *= (int64_t)group * bh_kv;
   // iterations per item: at least kDkdvMinChunk, and few enough that the whole
-  // grid has about kDkdvTargetItems items of work when columns are long
-  const int64_t chunk = std::max<int64_t>(kDkdvMinChunk, (total + kDkdvTargetItems - 1) / kDkdvTargetItems);
+  // grid has about kDkdvTargetItems items of work when columns are long; at
+  // most max_chunk when positive (a shorter fp32 accumulation per item)
+  int64_t chunk = std::max<int64_t>(kDkdvMinChunk, (total + kDkdvTargetItems - 1) / kDkdvTargetItems);
+  if (max_chunk > 0) chunk = std::min<int64_t>(chunk, max_chunk);
   int32_t ni = 0, ns = 0, np = 0;
   for (int kt = 0; kt < n_kt; ++kt) {
     const int64_t n_it = ((int64_t)col_ptr[kt + 1] - col_ptr[kt]) * group;
@@ -293,41 +356,12 @@ int gki_rolling_decode(const void* q, const void* k_cache, const void* v_cache, 
                        int32_t dtype, int32_t B, int32_t H, int32_t H_kv, int32_t n_q, int32_t head_dim,
                        int32_t sink_size, int32_t window_size, int32_t ring_size, int64_t length,
                        float softmax_scale, float* workspace, int32_t n_splits, void* stream) {
-  GKI_REQUIRE(dtype == kF32 || dtype == kF16 || dtype == kBF16, 2,
-              "unsupported dtype code " + std::to_string(dtype) + " (0=fp32, 1=fp16, 2=bf16)");
-  GKI_REQUIRE(head_dim == 64 || head_dim == 128, 2,
-              "gki_rolling_decode: head_dim must be 64 or 128, got " + std::to_string(head_dim));
-  GKI_REQUIRE(B > 0 && H > 0 && (int64_t)B * H < (1ll << 31) / 4096, 1,
-              "gki_rolling_decode: B and H must be positive and B * H not too large");
-  GKI_REQUIRE(H_kv > 0 && H % H_kv == 0, 1,
-              "H_kv must be positive and divide H (grouped-query attention)");
-  if (int rc = gki_rolling_stream(length, n_q, sink_size, window_size, ring_size, nullptr, nullptr,
-                                  nullptr))
+  if (int rc = rolling_decode_args(dtype, B, H, H_kv, n_q, head_dim, sink_size, window_size, ring_size,
+                                   length, softmax_scale, q, k_cache, v_cache, o, lse, n_splits))
     return rc;
-  GKI_REQUIRE(softmax_scale > 0.f && softmax_scale < __builtin_huge_valf(), 1,
-              "softmax_scale must be positive and finite");
-  GKI_REQUIRE(q && k_cache && v_cache && o && lse, 1, "gki_rolling_decode: null pointer");
-  GKI_REQUIRE(all_aligned16(q, k_cache, v_cache), 1, "gki_rolling_decode: q and caches must be 16-byte aligned");
-  GKI_REQUIRE(n_splits == 1 || workspace, 1, "gki_rolling_decode: null workspace");
-  GKI_REQUIRE(n_splits >= 1 && (int64_t)n_splits * B * H < (1ll << 31), 1,
-              "gki_rolling_decode: n_splits must be >= 1 and the grid must fit");
-  Geom g{};
-  g.B = B;
-  g.H = H;
-  g.H_kv = H_kv;
-  g.group = H / H_kv;
-  g.n_q = n_q;
-  g.n_kv = (int)length;                 // positions 0 .. length-1; queries are the last n_q
-  g.q_off = (int)length - n_q;
-  g.scale = softmax_scale;
-  g.scale_log2 = softmax_scale * kLog2e;
-  g.causal = 1;
-  g.sink = sink_size;
-  g.window = window_size;
-  g.mask = nullptr;                     // no stream entry carries the partial flag
-  g.n_qb = g.n_kb = g.bm = g.bn = 1;
-  return decode_ring_dispatch(dtype, head_dim, g, q, k_cache, v_cache, o, lse, ring_size, workspace,
-                              n_splits, (hipStream_t)stream);
+  return rolling_decode_checked(q, k_cache, v_cache, o, lse, dtype, B, H, H_kv, n_q, head_dim, sink_size,
+                                window_size, ring_size, length, softmax_scale, workspace, n_splits,
+                                stream);
 }
 
 }  // extern "C"

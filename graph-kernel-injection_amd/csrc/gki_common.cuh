@@ -76,6 +76,23 @@ __device__ inline floatx4 mfma_f32(float a, float b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// fp32 dot products over the head dimension on v_mfma_f32_16x16x4f32, KS
+// k-steps of 4: the steps go round-robin into NC independent accumulators,
+// summed pairwise at the end, so a long contraction (D = 128: 32 steps)
+// rounds like a quarter-length one. a(ks) / b(ks) give step ks's operands.
+template <int KS, typename FA, typename FB>
+__device__ inline floatx4 mfma_f32_dot(FA a, FB b) {
+  constexpr int NC = KS >= 16 ? 4 : (KS >= 4 ? 2 : 1);
+  floatx4 c[NC];
+#pragma unroll
+  for (int j = 0; j < NC; ++j) c[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) c[ks % NC] = mfma_f32(a(ks), b(ks), c[ks % NC]);
+  if constexpr (NC == 4) return (c[0] + c[1]) + (c[2] + c[3]);
+  else if constexpr (NC == 2) return c[0] + c[1];
+  else return c[0];
+}
+
 // 16-byte streaming (non-temporal) global load.
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 __device__ inline uint4 ld_nt16(const void* p) {
@@ -300,8 +317,16 @@ struct Geom {
   int B, H;
   int H_kv, group;    // K/V heads and q heads per K/V head (grouped-query attention; 1 = MHA)
   int n_q, n_kv, q_off;
-  float scale;        // natural-log softmax scale
+  float scale;        // natural-log softmax scale (any finite value)
   float scale_log2;   // scale * log2(e)
+  // The 16-bit prefill and matrix-core decode kernels track the running max
+  // on unscaled scores, which needs a positive scale. They read each 32-bit
+  // word w of Q as (w & q_and) ^ q_xor and scale by qk_scale_log2 instead:
+  // scale < 0 flips the sign of Q (exact: (-Q) K^T * |scale| equals
+  // Q K^T * scale bit for bit), scale == 0 zeroes Q (every score 0, as
+  // Q K^T * 0) with qk_scale_log2 = log2(e); scale > 0 leaves Q as it is.
+  float qk_scale_log2;
+  uint32_t q_and, q_xor;
   int causal, sink, window;
   // original block mask (used only for tiles flagged partial)
   const int32_t* mask;
@@ -323,6 +348,12 @@ struct KvWork {
   int n_pslots;           // partial slots per (b, kv head)
   float* partials;        // [B * H_kv][n_pslots][2 (dK, dV)][64][D] fp32
 };
+
+// A 16-byte Q fragment as the unscaled-max kernels read it (see Geom::q_and).
+__device__ inline uint4 q_words(const Geom& g, uint4 w) {
+  return make_uint4((w.x & g.q_and) ^ g.q_xor, (w.y & g.q_and) ^ g.q_xor, (w.z & g.q_and) ^ g.q_xor,
+                    (w.w & g.q_and) ^ g.q_xor);
+}
 
 // (b, q head) -> (b, kv head) row index of K / V (and dK / dV).
 __device__ inline int kv_bh(const Geom& g, int bh) {
@@ -547,7 +578,6 @@ __device__ inline float wave_sum16x4(float x) {
 }
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kNegInf = -__builtin_huge_valf();
 
 }  // namespace gki

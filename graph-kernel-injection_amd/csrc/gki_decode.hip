@@ -390,7 +390,7 @@ __global__ __launch_bounds__(64 * decode_waves<NQ>()) void decode_kernel(
     if (n_splits == 1) {
       const bool valid = L > 0.f;
       O[qb + (size_t)r * D + d] = T::from_float(valid ? a / L : 0.f);
-      if (d == 0) LSE[(size_t)bhq0 * g.n_q + r] = valid ? M * kLn2 + __logf(L) : 0.f;
+      if (d == 0) LSE[(size_t)bhq0 * g.n_q + r] = valid ? M + log2f(L) : 0.f;
     } else {
       part[r * row_stride + d] = a;
       if (d == 0) {
@@ -434,7 +434,7 @@ __global__ __launch_bounds__(64) void combine_kernel(const float* __restrict__ w
 #pragma unroll
   for (int j = 0; j < D / 64; ++j)
     O[(size_t)row * D + lane + 64 * j] = T::from_float(valid ? a[j] / L : 0.f);
-  if (lane == 0) LSE[row] = valid ? M * kLn2 + __logf(L) : 0.f;
+  if (lane == 0) LSE[row] = valid ? M + log2f(L) : 0.f;
 }
 
 template <typename T, int D, int NQ, typename Src>
@@ -587,7 +587,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(
     my_q[h] = r % g.n_q;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
-      qf[h][ks] = r < n_rows ? *(const uint4*)(Q + qb + (size_t)r * D + 32 * ks + 8 * grp)
+      qf[h][ks] = r < n_rows ? q_words(g, *(const uint4*)(Q + qb + (size_t)r * D + 32 * ks + 8 * grp))
                              : make_uint4(0, 0, 0, 0);
   }
   dma_wait();   // the Q loads are complete before any LDS-DMA is in flight
@@ -656,8 +656,8 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(
         s[h][i] = ok ? s[h][i] : kNegInf;
       }
       float mx = fmaxf(fmaxf(s[h][0], s[h][1]), fmaxf(s[h][2], s[h][3]));
-      if (__any(mx * g.scale_log2 > m[h] + kDecodeSlack)) {
-        mx = wave_max16x4(mx) * g.scale_log2;
+      if (__any(mx * g.qk_scale_log2 > m[h] + kDecodeSlack)) {   // unscaled max: Geom::q_and
+        mx = wave_max16x4(mx) * g.qk_scale_log2;
         const bool grow = mx > m[h] + kDecodeSlack;
         const float alpha = grow ? __builtin_amdgcn_exp2f(m[h] - mx) : 1.f;
         m[h] = grow ? mx : m[h];
@@ -668,7 +668,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(
       const float m_use = m[h] == kNegInf ? 0.f : m[h];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        s[h][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[h][i], g.scale_log2, -m_use));
+        s[h][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[h][i], g.qk_scale_log2, -m_use));
       lsum[h] += (s[h][0] + s[h][1]) + (s[h][2] + s[h][3]);
       pb[h] = make_uint2(pack2<T>(s[h][0], s[h][1]), pack2<T>(s[h][2], s[h][3]));
     }
@@ -718,7 +718,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(
       if (n_splits == 1) {
         const bool valid = L > 0.f;
         O[qb + (size_t)r * D + d] = T::from_float(valid ? a / L : 0.f);
-        if (d == 0) LSE[(size_t)bhq0 * g.n_q + r] = valid ? M * kLn2 + __logf(L) : 0.f;
+        if (d == 0) LSE[(size_t)bhq0 * g.n_q + r] = valid ? M + log2f(L) : 0.f;
       } else {
         part[r * row_stride + d] = a;
         if (d == 0) {

@@ -4,8 +4,11 @@
 // and its launch (sparse_triton_kernel.py:662-682). Semantics follow the
 // reference: S = (Q K^T) * scale in fp32, token mask (causal & (sink | window))
 // inside visited tiles, online softmax, P cast to V's dtype before P V,
-// O = acc / l, LSE = m + ln(l) with the (O = 0, LSE = 0) sentinel for rows that
-// saw no key (sparse_triton_kernel.py:341-352).
+// O = acc / l, LSE = m + log(l) with the (O = 0, LSE = 0) sentinel for rows that
+// saw no key (sparse_triton_kernel.py:341-352). The LSE is stored in base 2
+// (log2 of the row's sum of exp of the scaled scores, i.e. the natural LSE times
+// log2(e)): the running max m is already in base 2 and the backward consumes
+// the base-2 value directly, so no conversion rounds it twice.
 //
 // 16-bit design (one workgroup = 4 waves = one 128-row q tile; wave w owns rows
 // 32w .. 32w+31 as two 16-row blocks h = 0, 1):
@@ -22,6 +25,8 @@
 //    barrier per tile, the next tile's global loads in flight during the MFMAs.
 //  * Only kept tiles are visited (GPU-resident CSR list); the O^T rescale is
 //    skipped, exactly, when no row max of a block moved.
+//  * The running max is kept on unscaled scores, so Q is read through the
+//    Geom::q_and / q_xor transform that makes the effective scale positive.
 // The fp32 path uses v_mfma_f32_16x16x4f32 on 64-row tiles (16 rows per wave).
 #include "gki_common.cuh"
 
@@ -60,7 +65,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel_16(
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const int d0 = 32 * ks + 8 * grp;
-      qf[h][ks] = (q < g.n_q && d0 < D) ? *(const uint4*)(Q + qb + (size_t)q * D + d0)
+      qf[h][ks] = (q < g.n_q && d0 < D) ? q_words(g, *(const uint4*)(Q + qb + (size_t)q * D + d0))
                                         : make_uint4(0, 0, 0, 0);
     }
   }
@@ -143,10 +148,10 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel_16(
 #pragma unroll
         for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[h][t][i]);
       // A row's max exceeds the reference by the slack only if one of its
-      // lanes' maxima does (softmax_scale > 0, checked on the host, so scaling
-      // after the max is exact): the cross-lane reduction runs only then.
-      if (__any(mx * g.scale_log2 > m[h] + kRescaleSlack)) {
-        mx = wave_max16x4(mx) * g.scale_log2;
+      // lanes' maxima does (qk_scale_log2 > 0, so scaling after the max is
+      // exact): the cross-lane reduction runs only then.
+      if (__any(mx * g.qk_scale_log2 > m[h] + kRescaleSlack)) {
+        mx = wave_max16x4(mx) * g.qk_scale_log2;
         const bool grow = mx > m[h] + kRescaleSlack;
         const float alpha = grow ? __builtin_amdgcn_exp2f(m[h] - mx) : 1.f;
         m[h] = grow ? mx : m[h];
@@ -159,7 +164,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel_16(
       for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          s[h][t][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[h][t][i], g.scale_log2, -m_use));
+          s[h][t][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[h][t][i], g.qk_scale_log2, -m_use));
     }
 
 #pragma unroll
@@ -193,7 +198,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel_16(
         w.y = pack2<T>(o[h][dt][2] * inv, o[h][dt][3] * inv);
         *(uint2*)(O + qb + (size_t)my_q * D + 16 * dt + 4 * grp) = w;
       }
-      if (grp == 0) LSE[(size_t)bh * g.n_q + my_q] = valid ? m[h] * kLn2 + __logf(l_tot) : 0.f;
+      if (grp == 0) LSE[(size_t)bh * g.n_q + my_q] = valid ? m[h] + log2f(l_tot) : 0.f;
     }
   }
 }
@@ -279,10 +284,9 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel_32(
     floatx4 s[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      s[t] = floatx4{0.f, 0.f, 0.f, 0.f};
       const int r = rho(t, col);
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) s[t] = mfma_f32(sm.k[r * Smem::LD + 4 * ks + grp], qf[ks], s[t]);
+      s[t] = mfma_f32_dot<KS>([&](int ks) { return sm.k[r * Smem::LD + 4 * ks + grp]; },
+                              [&](int ks) { return qf[ks]; });
     }
     const bool need_mask = partial || (q0 + 15 >= g.n_q) || (k0 + kTileN > g.n_kv) ||
                            !tile_all_visible(g, q0, q_hi_wave, k0, k0 + kTileN - 1);
@@ -338,7 +342,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel_32(
       w.w = valid ? o[dt][3] / l_tot : o[dt][3];
       *(float4*)(O + qb + (size_t)my_q * D + 16 * dt + 4 * grp) = w;
     }
-    if (grp == 0) LSE[(size_t)bh * g.n_q + my_q] = valid ? m * kLn2 + __logf(l_tot) : 0.f;
+    if (grp == 0) LSE[(size_t)bh * g.n_q + my_q] = valid ? m + log2f(l_tot) : 0.f;
   }
 }
 

@@ -170,7 +170,8 @@ class StreamingKVCache:
                 lse.data_ptr(), _DTYPE_CODE[self.dtype], B, H, H_kv, n_q, self.head_dim, self.sink_size,
                 self.window_size, self.ring_size, self.length, float(softmax_scale), ws_ptr,
                 n_splits, stream), "gki_rolling_decode")
-        return (o, lse) if return_lse else o
+        # the kernels store the LSE in base 2; the API returns natural-log units
+        return (o, lse.mul_(math.log(2.0))) if return_lse else o
 
     def step(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
              softmax_scale: Optional[float] = None) -> torch.Tensor:

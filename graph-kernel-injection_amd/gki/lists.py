@@ -16,10 +16,9 @@ mask is turned once, on the GPU, into int32 lists:
   items whose fp32 partials are summed in order); the decode schedule adds the
   token-exact stream of visible positions.
 
-Schedules are cached per mask tensor (identity, version, geometry) and shared
-between tensors of equal content (one build per model, not per layer); the
-cache holds a reference to each mask so its storage cannot be recycled under
-the key. Building a schedule synchronises the stream once (to size the lists).
+Schedules are cached per mask content (one build per model, not per layer):
+each mask tensor is matched to a content class once, then found by identity.
+Building a schedule synchronises the stream once (to size the lists).
 """
 
 from __future__ import annotations
@@ -27,6 +26,7 @@ from __future__ import annotations
 import ctypes
 
 import threading
+import weakref
 from collections import OrderedDict
 from dataclasses import dataclass
 from typing import Tuple
@@ -38,7 +38,12 @@ from . import _lib
 
 @dataclass(frozen=True)
 class BlockLists:
-    """CSR + CSC kept-block lists of an int32 ``[n_rows, n_cols]`` matrix."""
+    """CSR + CSC kept-block lists of an int32 ``[n_rows, n_cols]`` matrix.
+
+    ``row_idx`` / ``col_idx`` are the nnz-long views; ``row_buf`` / ``col_buf``
+    their allocations (at least one element), whose addresses the kernels take:
+    an empty view reports a null data pointer, which the C ABI rejects, while
+    an empty list (nothing kept or visible) is legal and gives zero outputs."""
 
     row_ptr: torch.Tensor  # [n_rows + 1] int32
     row_idx: torch.Tensor  # [nnz] int32, column | partial << 30
@@ -47,6 +52,8 @@ class BlockLists:
     n_rows: int
     n_cols: int
     nnz: int
+    row_buf: torch.Tensor  # [max(nnz, 1)]
+    col_buf: torch.Tensor  # [max(nnz, 1)]
 
 
 @dataclass(frozen=True)
@@ -105,7 +112,8 @@ def _lists_of(matrix: torch.Tensor, need_cols: bool = True) -> BlockLists:
                                        col_ptr.data_ptr(), row_idx.data_ptr(),
                                        col_idx.data_ptr() if need_cols else None, stream),
                "gki_block_list_fill")
-    return BlockLists(row_ptr, row_idx[:nnz], col_ptr, col_idx[:nnz], n_rows, n_cols, nnz)
+    return BlockLists(row_ptr, row_idx[:nnz], col_ptr, col_idx[:nnz], n_rows, n_cols, nnz, row_idx,
+                      col_idx)
 
 
 def build_block_lists(block_mask: torch.Tensor) -> BlockLists:
@@ -138,51 +146,91 @@ def tile_matrix(mask: torch.Tensor, n_q: int, n_kv: int, block_m: int, block_n: 
 
 
 class _ScheduleCache:
-    """Schedules per mask tensor, shared across tensors of equal content.
+    """Schedules keyed by mask content, resolved once per mask tensor.
 
-    Lookup is by identity first (data pointer, version counter, shape, device).
-    On a miss the mask is compared (``torch.equal``, exact) with the cached
-    masks of the same shape, dtype, device and schedule key that have not been
-    modified in place since their schedule was built; a match reuses that
-    schedule. So the per-layer device copies of one injected mask (the FX pass
-    gives every ``_triton_attn_i`` its own buffer, which ``.to(device)`` copies
-    separately, fx_compiler_pass.py:346-368, 566, 592) share one schedule: one
-    list build per model instead of one per layer.
+    A mask tensor is mapped to a content class once per (tensor, version): on
+    later calls the alias table answers by identity (it sits outside the LRU
+    and holds the tensors weakly, so every layer's mask buffer stays resolved
+    however many layers a model has). An unresolved tensor is compared exactly
+    (``torch.equal``) with the representative of each known class of the same
+    shape, dtype and device; a match joins that class, otherwise the tensor
+    founds a new one. Schedules live in an LRU keyed by (class, schedule key).
+    So the per-layer device copies of one injected mask (the FX pass gives
+    every ``_triton_attn_i`` its own buffer, which ``.to(device)`` copies
+    separately, fx_compiler_pass.py:346-368, 566, 592) share one schedule per
+    key, and a steady-state step makes no comparison and no build.
+
+    A representative modified in place (version bump) retires its class and
+    the class's schedules. The class table holds each representative strongly,
+    so a retired mask's storage cannot be recycled under a live class.
     """
 
-    def __init__(self, capacity: int = 32) -> None:
-        self._d: "OrderedDict[tuple, Tuple[torch.Tensor, int, object]]" = OrderedDict()
+    def __init__(self, capacity: int = 64, max_classes: int = 16) -> None:
+        self._sched: "OrderedDict[tuple, object]" = OrderedDict()
+        self._classes: "OrderedDict[int, Tuple[torch.Tensor, int, tuple]]" = OrderedDict()
+        self._alias: dict = {}       # id(tensor) -> (weakref, version, class id)
+        self._next = 0
         self._cap = capacity
-        self._lock = threading.Lock()
+        self._max_classes = max_classes
+        self._lock = threading.RLock()
+
+    def _drop_class(self, cid: int) -> None:
+        self._classes.pop(cid, None)
+        for k in [k for k in self._sched if k[0] == cid]:
+            del self._sched[k]
+
+    def _forget(self, key: int, ref) -> None:
+        with self._lock:
+            ent = self._alias.get(key)
+            if ent is not None and ent[0] is ref:
+                del self._alias[key]
+
+    def _class_of(self, mask: torch.Tensor) -> int:
+        ent = self._alias.get(id(mask))
+        if ent is not None and ent[0]() is mask and ent[1] == mask._version:
+            cls = self._classes.get(ent[2])
+            if cls is not None and cls[0]._version == cls[1]:
+                self._classes.move_to_end(ent[2])
+                return ent[2]
+        meta = (tuple(mask.shape), mask.dtype, mask.device)
+        found = None
+        for cid, (rep, ver, m) in list(self._classes.items()):
+            if rep._version != ver:                      # representative changed in place
+                self._drop_class(cid)
+            elif found is None and m == meta and (rep is mask or torch.equal(rep, mask)):
+                found = cid
+        if found is None:
+            found = self._next
+            self._next += 1
+            self._classes[found] = (mask, mask._version, meta)
+            while len(self._classes) > self._max_classes:
+                self._drop_class(next(iter(self._classes)))
+        self._classes.move_to_end(found)
+        key = id(mask)
+        ref = weakref.ref(mask, lambda r, k=key: self._forget(k, r))
+        self._alias[key] = (ref, mask._version, found)
+        return found
 
     def get(self, mask: torch.Tensor, key: tuple, build):
-        full = (mask.data_ptr(), mask._version, tuple(mask.shape), mask.device) + key
-        content = (tuple(mask.shape), mask.dtype, mask.device) + key
         with self._lock:
-            hit = self._d.get(full)
-            if hit is not None and hit[0] is mask:
-                self._d.move_to_end(full)
-                return hit[2]
-            peers = [(m, ver, val) for k, (m, ver, val) in self._d.items()
-                     if k[2:] == full[2:] and m is not mask and m._version == ver
-                     and (tuple(m.shape), m.dtype, m.device) + key == content]
-        value = None
-        for m, _, val in peers:
-            if torch.equal(m, mask):
-                value = val
-                break
-        if value is None:
-            value = build()
+            full = (self._class_of(mask),) + key
+            hit = self._sched.get(full)
+            if hit is not None:
+                self._sched.move_to_end(full)
+                return hit
+        value = build()
         with self._lock:
-            self._d[full] = (mask, mask._version, value)
-            self._d.move_to_end(full)
-            while len(self._d) > self._cap:
-                self._d.popitem(last=False)
+            self._sched[full] = value
+            self._sched.move_to_end(full)
+            while len(self._sched) > self._cap:
+                self._sched.popitem(last=False)
         return value
 
     def clear(self) -> None:
         with self._lock:
-            self._d.clear()
+            self._sched.clear()
+            self._classes.clear()
+            self._alias.clear()
 
 
 _CACHE = _ScheduleCache()
@@ -208,43 +256,46 @@ def fwd_schedule(mask: torch.Tensor, n_q: int, n_kv: int, block_m: int, block_n:
     return _CACHE.get(mask, key, build)
 
 
-def dkdv_items(col_ptr_host: torch.Tensor, group: int, bh_kv: int):
+def dkdv_items(col_ptr_host: torch.Tensor, group: int, bh_kv: int, max_chunk: int = 0):
     """The dK/dV work list of CSC column pointers (a host int32 tensor):
     (items [n_items, 4], split [max(n_split, 1), 3], n_items, n_split, n_pslots),
-    host int32 tensors, from ``gki_dkdv_items``."""
+    host int32 tensors, from ``gki_dkdv_items`` (items of at most ``max_chunk``
+    iterations when positive)."""
     lib = _lib.load()
     ptr = col_ptr_host.to(torch.int32).contiguous()
     n_kt = ptr.numel() - 1
     counts = [ctypes.c_int32() for _ in range(3)]
     refs = [ctypes.addressof(c) for c in counts]
-    _lib.check(lib.gki_dkdv_items(ptr.data_ptr(), n_kt, group, bh_kv, None, refs[0], None, refs[1],
-                                  refs[2]), "gki_dkdv_items")
+    _lib.check(lib.gki_dkdv_items(ptr.data_ptr(), n_kt, group, bh_kv, max_chunk, None, refs[0], None,
+                                  refs[1], refs[2]), "gki_dkdv_items")
     n_items, n_split, _ = (c.value for c in counts)
     items = torch.empty((n_items, 4), dtype=torch.int32)
     split = torch.zeros((max(n_split, 1), 3), dtype=torch.int32)
-    _lib.check(lib.gki_dkdv_items(ptr.data_ptr(), n_kt, group, bh_kv, items.data_ptr(), refs[0],
-                                  split.data_ptr(), refs[1], refs[2]), "gki_dkdv_items")
+    _lib.check(lib.gki_dkdv_items(ptr.data_ptr(), n_kt, group, bh_kv, max_chunk, items.data_ptr(),
+                                  refs[0], split.data_ptr(), refs[1], refs[2]), "gki_dkdv_items")
     return items, split, counts[0].value, counts[1].value, counts[2].value
 
 
 def bwd_schedule(mask: torch.Tensor, n_q: int, n_kv: int, block_m: int, block_n: int,
                  is_causal: bool, sink: int, window: int, group: int = 1,
-                 bh_kv: int = 1) -> BwdSchedule:
+                 bh_kv: int = 1, max_chunk: int = 0) -> BwdSchedule:
     """CSR + CSC schedules of the dQ and dK/dV kernels (64x64 tiles) and the
     dK/dV work list for ``group`` q heads per kv head over ``bh_kv`` = B * H_kv
-    (b, kv head) pairs."""
+    (b, kv head) pairs (items of at most ``max_chunk`` iterations when positive)."""
     ts = _lib.tile_sizes()
     tm, tn = ts["bwd_tile_m"], ts["tile_n"]
 
     def build() -> BwdSchedule:
         tiles = tile_matrix(mask, n_q, n_kv, block_m, block_n, tm, tn, is_causal, sink, window)
         lists = _lists_of(tiles)
-        items, split, n_items, n_split, n_pslots = dkdv_items(lists.col_ptr.cpu(), group, bh_kv)
+        items, split, n_items, n_split, n_pslots = dkdv_items(lists.col_ptr.cpu(), group, bh_kv,
+                                                              max_chunk)
         dev = mask.device
         return BwdSchedule(lists, items.to(dev), n_items, split.to(dev), n_split, n_pslots,
                            lists.n_rows, lists.n_cols)
 
-    key = ("bwd", n_q, n_kv, block_m, block_n, tm, tn, bool(is_causal), sink, window, group, bh_kv)
+    key = ("bwd", n_q, n_kv, block_m, block_n, tm, tn, bool(is_causal), sink, window, group, bh_kv,
+           max_chunk)
     return _CACHE.get(mask, key, build)
 
 
@@ -262,7 +313,7 @@ def decode_schedule(mask: torch.Tensor, n_q: int, n_kv: int, block_m: int, block
         tokens = torch.empty(max(lists.nnz * tn, 1), dtype=torch.int32, device=mask.device)
         count = torch.zeros(1, dtype=torch.int32, device=mask.device)
         n_qb, n_kb = (int(s) for s in mask.shape)
-        _lib.check(lib.gki_decode_tokens(lists.row_idx.data_ptr(), lists.nnz, n_q, n_kv,
+        _lib.check(lib.gki_decode_tokens(lists.row_buf.data_ptr(), lists.nnz, n_q, n_kv,
                                          mask.data_ptr(), n_qb, n_kb, block_m, block_n,
                                          int(bool(is_causal)), sink, window, tokens.data_ptr(),
                                          count.data_ptr(), _stream(mask.device)), "gki_decode_tokens")
@@ -270,7 +321,7 @@ def decode_schedule(mask: torch.Tensor, n_q: int, n_kv: int, block_m: int, block
         toks = tokens[:n_tokens]
         ring = 0
         r = n_kv - sink
-        if is_causal and r >= 1 and r >= window + n_q - 1 and n_kv < (1 << 30):
+        if is_causal and n_kv >= n_q and r >= 1 and r >= window + n_q - 1 and n_kv < (1 << 30):
             a, b, c = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
             _lib.check(lib.gki_rolling_stream(n_kv, n_q, sink, window, r, ctypes.byref(a),
                                               ctypes.byref(b), ctypes.byref(c)), "gki_rolling_stream")

@@ -170,7 +170,7 @@ def _attention_forward(q, k, v, block_mask, softmax_scale, block_m, block_n, is_
             _lib.check(lib.gki_bsa_fwd(
                 q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), dtype,
                 B, H, H_kv, N_Q, N_KV, D, sched.lists.row_ptr.data_ptr(),
-                sched.lists.row_idx.data_ptr(), sched.n_qt, *common, stream), "gki_bsa_fwd")
+                sched.lists.row_buf.data_ptr(), sched.n_qt, *common, stream), "gki_bsa_fwd")
 
     return o, lse, q, k, v, block_mask, q_offset
 
@@ -238,7 +238,7 @@ class _BlockSparseFlashAttention(torch.autograd.Function):
                 q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(),
                 lse.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), delta.data_ptr(),
                 _DTYPE_CODE[q.dtype], B, H, H_kv, N_Q, N_KV, D, L.row_ptr.data_ptr(),
-                L.row_idx.data_ptr(), sched.n_qt, L.col_ptr.data_ptr(), L.col_idx.data_ptr(),
+                L.row_buf.data_ptr(), sched.n_qt, L.col_ptr.data_ptr(), L.col_buf.data_ptr(),
                 sched.n_kt, sched.items.data_ptr(), sched.n_items, sched.split.data_ptr(),
                 sched.n_split, sched.n_pslots, partials.data_ptr(), block_mask.data_ptr(), n_qb,
                 n_kb, ctx.block_m, ctx.block_n, float(ctx.softmax_scale), int(ctx.is_causal),

@@ -6,6 +6,11 @@
  *  - Tensors are device pointers to contiguous [B, H, N, D] arrays (BHND,
  *    row-major), as produced by `.contiguous()` in the reference
  *    (sparse_triton_kernel.py:834). LSE / Delta are contiguous fp32 [B, H, N_Q].
+ *  - LSE is stored in base 2: log2 of each row's sum of exp of its scaled
+ *    scores, i.e. the natural log-sum-exp times log2(e) (0 for rows that see
+ *    no key, as the reference's sentinel, sparse_triton_kernel.py:341-352).
+ *    The kernels keep the running max in base 2 and the backward consumes the
+ *    value as is, so it is rounded once instead of three times.
  *  - Grouped-query attention: Q / O / dQ have H heads, K / V / dK / dV have
  *    H_kv heads, H_kv dividing H; q head h reads kv head h / (H / H_kv).
  *    H_kv == H is the reference's multi-head case (the reference rejects any
@@ -37,8 +42,8 @@
 extern "C" {
 #endif
 
-/* ABI version (currently 3: grouped-query attention, H_kv after H; dK/dV work
- * items from gki_dkdv_items). */
+/* ABI version (currently 4: grouped-query attention, H_kv after H; dK/dV work
+ * items from gki_dkdv_items, whose chunk can be capped by max_chunk). */
 int gki_abi_version(void);
 
 /* Message of the last failing call on this thread. */
@@ -95,19 +100,20 @@ int gki_block_list_fill(const int32_t* m, int32_t n_rows, int32_t n_cols,
  * col_ptr: the CSC column pointers (n_kt + 1, host copy) of the backward tiles;
  * group: q heads per K/V head; bh_kv: B * H_kv. A kv tile's walk of
  * group x (its list length) iterations becomes one item, or -- when longer than
- * the chunk max(32, ceil(total iterations / 8192)) -- several near-equal items
- * whose fp32 partials gki_bsa_bwd sums in item order (deterministic). Writes
+ * the chunk max(32, ceil(total iterations / 8192)), capped at max_chunk when
+ * max_chunk > 0 -- several near-equal items whose fp32 partials gki_bsa_bwd
+ * sums in item order (deterministic; fp32 partials with a compensated sum). Writes
  * items [n_items][4] = (kv tile, first iteration, end iteration, partial slot or
  * -1) and split [n_split][3] = (kv tile, first slot, slot count), and the counts;
  * pass items = split = NULL to size them first. n_pslots partial slots per
  * (b, kv head) need 2 * 64 * head_dim floats each. */
 int gki_dkdv_items(const int32_t* col_ptr, int32_t n_kt, int32_t group, int32_t bh_kv,
-                   int32_t* items, int32_t* n_items, int32_t* split, int32_t* n_split,
-                   int32_t* n_pslots);
+                   int32_t max_chunk, int32_t* items, int32_t* n_items, int32_t* split,
+                   int32_t* n_split, int32_t* n_pslots);
 
 /* Prefill forward: replaces the `_fwd_kernel` launch in
  * `_BlockSparseFlashAttention.forward` (sparse_triton_kernel.py:662-682).
- * O = softmax(mask(Q K^T * scale)) V, LSE = m + ln(l) (0 for empty rows).
+ * O = softmax(mask(Q K^T * scale)) V, LSE (base 2) = m + log2(l), 0 for empty rows.
  * row_ptr/row_idx: CSR over ceil(n_q/fwd_tile_m) q tiles (fwd_tile_m_16 or
  * fwd_tile_m_32 by dtype) of kept kv tiles. */
 int gki_bsa_fwd(const void* q, const void* k, const void* v, void* o, float* lse,

@@ -146,20 +146,23 @@ def tile_classes(mask: np.ndarray, n_q: int, n_kv: int, bm: int, bn: int, tm: in
 
 
 def dkdv_items(col_ptr: np.ndarray, group: int, bh_kv: int, chunk: Optional[int] = None,
-               min_chunk: int = 32, target_items: int = 8192):
+               min_chunk: int = 32, target_items: int = 8192, max_chunk: int = 0):
     """The dK/dV work list (build-only; the reference runs one program per kv
     tile, sparse_triton_kernel.py:719-777). A kv tile's walk of group x (its
     column length) iterations is one item (slot -1) when it fits the chunk,
     else ``parts = ceil(n_it / chunk)`` items ``[n_it*c/parts, n_it*(c+1)/parts)``
     writing consecutive partial slots. ``chunk`` defaults to
     ``max(min_chunk, ceil(total / target_items))`` with
-    ``total = sum(len) * group * bh_kv``. Returns (items [n, 4], split [m, 3],
+    ``total = sum(len) * group * bh_kv``, then ``min(chunk, max_chunk)`` when
+    ``max_chunk > 0``. Returns (items [n, 4], split [m, 3],
     n_pslots) as int32 arrays: items (kv tile, first, end, slot | -1), split
     (kv tile, first slot, slot count)."""
     cnt = np.diff(col_ptr.astype(np.int64))
     if chunk is None:
         total = int(cnt.sum()) * group * bh_kv
         chunk = max(min_chunk, -(-total // target_items))
+        if max_chunk > 0:
+            chunk = min(chunk, max_chunk)
     items, split, n_pslots = [], [], 0
     for kt, n in enumerate(cnt):
         n_it = int(n) * group

@@ -60,9 +60,31 @@ def test_config2_flops_are_the_kept_block_count():
     assert 4 * 64 * 64 * 128 * kept * 32 == 546467479552
 
 
+def test_block_granular_bytes_count_the_ragged_last_tile():
+    """Config 4: 34 kept 64-key tiles, the last (1562) holding 100000 - 99968 =
+    32 tokens: 2144 tokens x 128 x 2 tensors x 2 B x 256 heads = 281,018,368 B."""
+    import torch
+
+    from oracle import streaming_oracle as so
+
+    row = torch.from_numpy(so.block_mask(1, 100000, 4, 2048, 1, 64))[0]
+    assert int(row.sum()) == 34
+    tokens = bench.block_granular_tokens(row, 100000, 64)
+    assert tokens == 33 * 64 + 32
+    assert tokens * 128 * 2 * 2 * 8 * 32 == 281018368
+
+
+def test_cpu_threads_follow_the_allotted_share(monkeypatch):
+    monkeypatch.setenv("OMP_NUM_THREADS", "3")
+    assert bench.cpu_threads() == min(3, len(os.sched_getaffinity(0)))
+    monkeypatch.delenv("OMP_NUM_THREADS")
+    assert bench.cpu_threads() == len(os.sched_getaffinity(0))
+
+
 def test_cpu_baseline_leg_on_a_small_sample():
-    """The timed leg runs the oracle's eager path (S 4, W 2048, 64x64 blocks, as
-    config 2) head by head within its budget and reports kept-block TFLOP/s."""
+    """The timed leg runs the oracle's eager path head by head within its
+    budget: config-2-like forward (kept-block TFLOP/s), config-3-like forward +
+    backward, and a config-4-like decode slice (kept K/V GB/s)."""
     import torch
 
     from oracle import streaming_oracle as so
@@ -71,7 +93,17 @@ def test_cpu_baseline_leg_on_a_small_sample():
     q, k, v = (torch.randn(1, 2, 512, 64, generator=g) * 0.5 for _ in range(3))
     mask = torch.from_numpy(so.block_mask(512, 512, 4, 2048, 64, 64))
     kept = int(mask.sum())
-    out = bench.cpu_baseline((q, k, v, mask), kept, budget_s=0.5)
+    q3, k3, v3, do3 = (torch.randn(2, 1, 256, 64, generator=g).half() for _ in range(4))
+    m3 = torch.from_numpy(so.block_mask(256, 256, 4, 1024, 64, 64))
+    q4 = torch.randn(1, 2, 1, 128, generator=g).bfloat16()
+    k4, v4 = (torch.randn(1, 2, 3000, 128, generator=g).bfloat16() for _ in range(2))
+    m4 = torch.from_numpy(so.block_mask(1, 3000, 4, 2048, 1, 64))
+    extra = {"c3": (q3, k3, v3, do3, m3, int(m3.sum())), "c4": (q4, k4, v4, m4)}
+    out = bench.cpu_baseline((q, k, v, mask), kept, budget_s=0.5, extra=extra)
     assert out["kind"] == "port" and out["unit"] == "TFLOP/s"
-    assert out["value"] > 0 and out["cores"] >= 1
+    assert out["value"] > 0 and out["cores"] == bench.cpu_threads()
+    assert out["cpu_model"] and out["os_cpu_count"] == os.cpu_count()
     assert "of 2 heads" in out["sample"]
+    assert out["c3"]["unit"] == "TFLOP/s" and out["c3"]["value"] > 0
+    assert "of 2 (b, h) slices" in out["c3"]["sample"]
+    assert out["c4"]["unit"] == "GB/s" and out["c4"]["value"] > 0

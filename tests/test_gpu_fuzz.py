@@ -12,11 +12,16 @@ oracle's closed forms (sparse_triton_kernel.py:845-902 semantics).
 Inputs at the configs' scales (N(0,1) times 0.5 or 1) are held to the
 element-wise tolerances the parity tests use: fp32 atol 1e-5; fp16 / bf16
 atol 2e-2 + rtol 1e-2. Inputs times 2 (logits of standard deviation ~4,
-gradients ~20) are held to a magnitude-relative bound instead, relative
-Frobenius error <= 1e-5 (fp32) / 1e-2 (fp16, bf16): fixed absolute bounds do
-not scale with the values, and the kernels' error there is rounding-level
-(~1e-6 fp32, ~5e-3 bf16, where 16-bit P and dS are rounded as the reference
-rounds them).
+gradients ~20) are outside the range those fixed bounds were set for, so the
+case also runs the reference's own eager path (``reference_block_sparse_attention``,
+sparse_triton_kernel.py:845-902, in the input dtype on the CPU, gradients by
+autograd) as a control: every element of the kernel's result must lie within
+max(the fixed tolerance, 2 x the eager path's worst error on the same tensor)
+of the fp64 oracle. At these magnitudes the fp32 rounding of the scores Q K^T
+dominates every result, so the eager path's own error moves by up to ~3x with
+the order of the head-dimension sum alone; the control therefore takes its
+worst error over four such orders (the identity and three fixed permutations
+of the head dimension of Q and K, which leave the mathematics unchanged).
 """
 
 from __future__ import annotations
@@ -32,7 +37,6 @@ from oracle import streaming_oracle as so
 
 DEV = "cuda"
 TOL = {torch.float32: (1e-5, 0.0), torch.float16: (2e-2, 1e-2), torch.bfloat16: (2e-2, 1e-2)}
-REL = {torch.float32: 1e-5, torch.float16: 1e-2, torch.bfloat16: 1e-2}
 BLOCKS = [1, 2, 8, 16, 32, 64, 128]
 N_CASES = 96
 
@@ -59,18 +63,54 @@ def _case(seed):
                 mask_seed=int(rng.integers(0, 1 << 30)))
 
 
-def _close(ours, ref, dtype, what, elementwise):
+def _close(ours, ref, dtype, what, eager=None):
+    """Element-wise |ours - ref| <= atol + rtol |ref|, widened to twice the
+    eager control's worst error on the same tensor when one is given."""
     o = ours.detach().to(torch.float64).cpu()
     r = torch.as_tensor(ref).to(torch.float64)
     assert torch.isfinite(o).all(), what
-    rel = ((o - r).norm() / r.norm().clamp_min(1e-30)).item() if r.abs().max() > 0 else o.abs().max().item()
-    info = f"max err {(o - r).abs().max():.3e}, max |ref| {r.abs().max():.3e}, relative Frobenius error {rel:.2e}"
-    if elementwise:
-        atol, rtol = TOL[dtype]
-        bad = (o - r).abs() > atol + rtol * r.abs()
-        assert not bad.any(), f"{what}: {int(bad.sum())} out of tolerance, {info}"
-    else:
-        assert rel <= REL[dtype], f"{what}: {info}"
+    atol, rtol = TOL[dtype]
+    bound = atol + rtol * r.abs()
+    info = f"max err {(o - r).abs().max():.3e}, max |ref| {r.abs().max():.3e}"
+    if eager is not None:
+        e_err = float((eager.detach().to(torch.float64).cpu() - r).abs().max())
+        bound = bound.clamp_min(2.0 * e_err)
+        info += f", eager control max err {e_err:.3e}"
+    bad = (o - r).abs() > bound
+    assert not bad.any(), f"{what}: {int(bad.sum())} out of tolerance, {info}"
+
+
+def _eager_once(q, k, v, do, mask, group, c, perm):
+    """The reference's eager path on the CPU in the input dtype, the head
+    dimension of Q and K taken in the order ``perm`` (K / V expanded per q
+    head; autograd sums the expanded gradients back): O, dQ, dK, dV."""
+    from gki.reference import reference_block_sparse_attention
+
+    inv = torch.argsort(perm)
+    leaves = [t.detach().cpu().clone().requires_grad_(True) for t in (q[..., perm], k[..., perm], v)]
+    kx, vx = (t.repeat_interleave(group, dim=1) for t in leaves[1:])
+    out = reference_block_sparse_attention(leaves[0], kx, vx, mask.cpu(), block_m=c["bm"],
+                                           block_n=c["bn"], is_causal=c["causal"],
+                                           sink_size=c["sink"], window_size=c["window"],
+                                           softmax_scale=1.0 / math.sqrt(q.shape[-1]))
+    out.backward(do.cpu())
+    return [out.detach(), leaves[0].grad[..., inv], leaves[1].grad[..., inv], leaves[2].grad]
+
+
+def _eager_control(q, k, v, do, mask, group, c, refs):
+    """Per result tensor, the eager path's run with the largest error against
+    ``refs`` over four head-dimension orders (see the module docstring)."""
+    D = q.shape[-1]
+    rng = np.random.default_rng(D)
+    perms = [torch.arange(D)] + [torch.from_numpy(rng.permutation(D)) for _ in range(3)]
+    worst = [None] * 4
+    for perm in perms:
+        res = _eager_once(q, k, v, do, mask, group, c, perm)
+        for i, (t, r) in enumerate(zip(res, refs)):
+            err = float((t.to(torch.float64) - torch.as_tensor(r)).abs().max())
+            if worst[i] is None or err > worst[i][0]:
+                worst[i] = (err, t)
+    return [w[1] for w in worst]
 
 
 @pytest.mark.gpu
@@ -101,8 +141,10 @@ def test_random_case_matches_oracle(seed):
     s = 1.0 / math.sqrt(D)
     o_ref, _ = so.attention_fwd(qn, kx, vx, eff, s)
     dq, dk, dv = so.attention_bwd(qn, kx, vx, don, eff, s)
-    tag, ew = f"seed {seed}", c["scale"] <= 1.0
-    _close(out, o_ref, dtype, "O " + tag, ew)
-    _close(leaves[0].grad, dq, dtype, "dQ " + tag, ew)
-    _close(leaves[1].grad, so.reduce_kv_grad(dk, group), dtype, "dK " + tag, ew)
-    _close(leaves[2].grad, so.reduce_kv_grad(dv, group), dtype, "dV " + tag, ew)
+    tag = f"seed {seed}"
+    refs = [o_ref, dq, so.reduce_kv_grad(dk, group), so.reduce_kv_grad(dv, group)]
+    ctl = [None] * 4
+    if c["scale"] > 1.0:
+        ctl = _eager_control(q, k, v, do, mask, group, c, refs)
+    for name, got, ref, e in zip(("O", "dQ", "dK", "dV"), [out] + [t.grad for t in leaves], refs, ctl):
+        _close(got, ref, dtype, f"{name} {tag}", e)

@@ -94,7 +94,7 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(lib, name), f"{name} declared in gki_bsa.h but not exported"
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
     assert set(_lib.SIGNATURES) == set(names)
-    assert lib.gki_abi_version() == 3
+    assert lib.gki_abi_version() == 4
 
 
 def test_dkdv_work_list_matches_oracle():
@@ -112,13 +112,19 @@ def test_dkdv_work_list_matches_oracle():
                       int(rng.integers(1, 128))))
     m = so.block_mask(131072, 131072, 4, 4096, 64, 64)
     cases.append((so.kept_lists(m)[2], 1, 16))
-    for col_ptr, group, bh_kv in cases:
+    for i, (col_ptr, group, bh_kv) in enumerate(cases):
         col_ptr = col_ptr.astype(np.int32)
-        items, split, n_items, n_split, n_pslots = dkdv_items(torch.from_numpy(col_ptr), group, bh_kv)
-        want_items, want_split, want_np = so.dkdv_items(col_ptr, group, bh_kv)
-        np.testing.assert_array_equal(items.numpy(), want_items)
-        assert n_items == len(want_items) and n_split == len(want_split) and n_pslots == want_np
-        np.testing.assert_array_equal(split.numpy()[:n_split], want_split)
+        # uncapped (16-bit inputs), the fp32 cap, and caps above the default chunk
+        for max_chunk in (0, 4, 1 + i % 50):
+            items, split, n_items, n_split, n_pslots = dkdv_items(torch.from_numpy(col_ptr), group,
+                                                                  bh_kv, max_chunk)
+            want_items, want_split, want_np = so.dkdv_items(col_ptr, group, bh_kv,
+                                                            max_chunk=max_chunk)
+            np.testing.assert_array_equal(items.numpy(), want_items)
+            assert n_items == len(want_items) and n_split == len(want_split) and n_pslots == want_np
+            np.testing.assert_array_equal(split.numpy()[:n_split], want_split)
+            if max_chunk > 0:
+                assert (want_items[:, 2] - want_items[:, 1]).max(initial=0) <= max_chunk
 
 
 def test_decode_routing_rules():
@@ -150,10 +156,10 @@ def test_dkdv_work_list_rejects_bad_columns():
     out = [ctypes.c_int32() for _ in range(3)]
     refs = [ctypes.addressof(c) for c in out]
     bad = np.array([0, 5, 3], np.int32)                         # decreasing pointer
-    assert lib.gki_dkdv_items(bad.ctypes.data, 2, 1, 1, None, refs[0], None, refs[1], refs[2]) == 1
+    assert lib.gki_dkdv_items(bad.ctypes.data, 2, 1, 1, 0, None, refs[0], None, refs[1], refs[2]) == 1
     assert b"column" in lib.gki_last_error()
     ok = np.array([0, 5], np.int32)
-    assert lib.gki_dkdv_items(ok.ctypes.data, 1, 0, 1, None, refs[0], None, refs[1], refs[2]) == 1
+    assert lib.gki_dkdv_items(ok.ctypes.data, 1, 0, 1, 0, None, refs[0], None, refs[1], refs[2]) == 1
 
 
 def test_tile_sizes():

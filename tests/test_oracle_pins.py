@@ -241,6 +241,9 @@ def test_dkdv_work_list_invariants():
             items, split, n_pslots = so.dkdv_items(col_ptr, group, bh_kv, chunk=chunk)
             c = chunk or max(32, -(-int(cnt.sum()) * group * bh_kv // 8192))
             _check_work_list(col_ptr, group, items, split, n_pslots, c)
+        # a cap below the default chunk (the fp32 work list) bounds every item
+        items, split, n_pslots = so.dkdv_items(col_ptr, group, bh_kv, max_chunk=4)
+        _check_work_list(col_ptr, group, items, split, n_pslots, 4)
 
 
 def test_dkdv_work_list_splits_only_long_columns():

@@ -83,3 +83,46 @@ def test_injected_layers_build_one_schedule(monkeypatch):
         ref = stk.block_sparse_attention(ref, k, v, masks[0], is_causal=True, sink_size=4,
                                          window_size=128)
     assert torch.equal(out, ref)
+
+
+def test_many_layers_steady_state_makes_no_comparison_and_no_build(monkeypatch):
+    """24 layers, each with its own copy of one mask, fwd + bwd schedules per
+    step: the first step resolves every copy once (one comparison each) and
+    builds two schedules; later steps neither compare nor build."""
+    import gki.lists as lists
+
+    c, calls = _ScheduleCache(), []
+    base = torch.randint(0, 2, (32, 32), dtype=torch.int32)
+    layers = [base.clone() for _ in range(24)]
+    compares = []
+    orig_equal = torch.equal
+
+    def counting_equal(a, b):
+        compares.append(1)
+        return orig_equal(a, b)
+
+    monkeypatch.setattr(lists.torch, "equal", counting_equal)
+
+    def step():
+        for m in layers:
+            assert c.get(m, ("fwd",), _builder(calls, "F")) == "F"
+        for m in reversed(layers):
+            assert c.get(m, ("bwd",), _builder(calls, "B")) == "B"
+
+    step()
+    assert calls == ["F", "B"] and len(compares) == 23
+    for _ in range(3):
+        step()
+    assert calls == ["F", "B"] and len(compares) == 23
+
+
+def test_dead_masks_leave_the_alias_table():
+    """50 short-lived masks of 3 contents: 3 classes (their first tensors are
+    the representatives, held by the class table), 3 builds, and only the
+    representatives' aliases left."""
+    c, calls = _ScheduleCache(), []
+    for i in range(50):
+        m = torch.full((4, 4), i % 3, dtype=torch.int32)
+        assert c.get(m, ("k",), _builder(calls, i)) == i % 3
+        del m
+    assert calls == [0, 1, 2] and len(c._classes) == 3 and len(c._alias) == 3
