@@ -6,6 +6,7 @@
 // allocates or frees device memory and keeps no pointer after returning.
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 
 #include "gki_bsa.h"
 #include "gki_common.cuh"
@@ -104,6 +105,38 @@ int make_geom(Geom& g, int dtype, int B, int H, int H_kv, int n_q, int n_kv, int
   g.n_kb = n_kb;
   g.bm = block_m;
   g.bn = block_n;
+  return 0;
+}
+
+// Device-resident scratch of gki_rolling_decode_noalloc (the split partials
+// of a decode step), for callers that cannot allocate: code under HIP graph
+// capture, tight serving loops. Every GPU the library runs on holds its own
+// copy until the process ends. In host code `scratch` names a host-side
+// stand-in, never the device array: the device address comes from
+// hipGetSymbolAddress, once per device (scratch_on_current_device).
+constexpr int64_t kScratchFloats = int64_t(4) << 20;   // 16 MiB
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's scratch address (looked up on first use per device,
+// with that device current).
+int scratch_on_current_device(float** out) {
+  int dev = -1;
+  const hipError_t e0 = hipGetDevice(&dev);
+  GKI_REQUIRE(e0 == hipSuccess && dev >= 0 && dev < kMaxDevices, 3,
+              std::string("scratch: no current HIP device (") + hipGetErrorString(e0) + ")");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    GKI_REQUIRE(e == hipSuccess && p != nullptr, 3,
+                std::string("scratch: hipGetSymbolAddress failed: ") + hipGetErrorString(e));
+    g_scratch_ptr[dev] = (float*)p;
+  }
+  *out = g_scratch_ptr[dev];
   return 0;
 }
 
@@ -362,6 +395,28 @@ int gki_rolling_decode(const void* q, const void* k_cache, const void* v_cache, 
   return rolling_decode_checked(q, k_cache, v_cache, o, lse, dtype, B, H, H_kv, n_q, head_dim, sink_size,
                                 window_size, ring_size, length, softmax_scale, workspace, n_splits,
                                 stream);
+}
+
+int gki_rolling_decode_noalloc(const void* q, const void* k_cache, const void* v_cache, void* o,
+                               float* lse, int32_t dtype, int32_t B, int32_t H, int32_t H_kv,
+                               int32_t n_q, int32_t head_dim, int32_t sink_size, int32_t window_size,
+                               int32_t ring_size, int64_t length, float softmax_scale, int32_t n_splits,
+                               void* stream) {
+  if (int rc = rolling_decode_args(dtype, B, H, H_kv, n_q, head_dim, sink_size, window_size, ring_size,
+                                   length, softmax_scale, q, k_cache, v_cache, o, lse, n_splits))
+    return rc;
+  float* ws = nullptr;
+  if (n_splits > 1) {
+    const int64_t need = gki_bsa_decode_workspace_floats(B, H, n_q, head_dim, n_splits);
+    GKI_REQUIRE(need <= kScratchFloats, 1,
+                "gki_rolling_decode_noalloc: n_splits * B * H * n_q * (head_dim + 2) = " +
+                    std::to_string(need) + " floats exceeds the library scratch of " +
+                    std::to_string(kScratchFloats) + " floats (16 MiB); use fewer splits or "
+                    "gki_rolling_decode with a workspace");
+    if (int rc = scratch_on_current_device(&ws)) return rc;
+  }
+  return rolling_decode_checked(q, k_cache, v_cache, o, lse, dtype, B, H, H_kv, n_q, head_dim, sink_size,
+                                window_size, ring_size, length, softmax_scale, ws, n_splits, stream);
 }
 
 }  // extern "C"

@@ -48,6 +48,8 @@ SIGNATURES = {
     "gki_rolling_append": (ctypes.c_int, [_c_ptr] * 4 + [_c_int] * 6 + [_c_i64, _c_int, _c_ptr]),
     "gki_rolling_decode": (ctypes.c_int, [_c_ptr] * 5 + [_c_int] * 9 + [_c_i64, _c_float, _c_ptr,
                                                                        _c_int, _c_ptr]),
+    "gki_rolling_decode_noalloc": (ctypes.c_int, [_c_ptr] * 5 + [_c_int] * 9
+                                   + [_c_i64, _c_float, _c_int, _c_ptr]),
 }
 
 _lock = threading.Lock()

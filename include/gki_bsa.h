@@ -214,6 +214,23 @@ int gki_rolling_decode(const void* q, const void* k_cache, const void* v_cache, 
                        int32_t ring_size, int64_t length, float softmax_scale,
                        float* workspace, int32_t n_splits, void* stream);
 
+/* gki_rolling_decode without a workspace argument: the split partials
+ * (gki_bsa_decode_workspace_floats(B, H, n_q, head_dim, n_splits) floats when
+ * n_splits > 1) live in a library-owned device array of 4194304 floats
+ * (16 MiB), one per GPU, held until the process ends; larger requests return
+ * 1 with a message and launch nothing. The call allocates nothing (no hipMalloc,
+ * no allocating library routine). Same kernels, stream order and results as
+ * gki_rolling_decode with the same n_splits. Calls that overlap on one GPU
+ * (other streams, other threads) share the array and race; serialise them.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation). */
+int gki_rolling_decode_noalloc(const void* q, const void* k_cache, const void* v_cache, void* o,
+                               float* lse, int32_t dtype, int32_t B, int32_t H, int32_t H_kv,
+                               int32_t n_q, int32_t head_dim, int32_t sink_size,
+                               int32_t window_size, int32_t ring_size, int64_t length,
+                               float softmax_scale, int32_t n_splits, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
