@@ -226,10 +226,11 @@ def measure_errors(cfg: HarnessConfig) -> Dict[str, Optional[float]]:
     return errors
 
 
-def verdict(ours: BenchResult, flex: Optional[BenchResult]) -> str:
-    """Win / tie / loss against FlexAttention (docs/eval_plan.md §5)."""
+def verdict(ours: BenchResult, flex: Optional[BenchResult], flex_error: Optional[str] = None) -> str:
+    """Win / tie / loss against FlexAttention (docs/eval_plan.md §5); without a
+    FlexAttention result, "no verdict" and why (``flex_error``)."""
     if flex is None:
-        return "no FlexAttention result: no verdict"
+        return "no FlexAttention result: no verdict" + (f" ({flex_error})" if flex_error else "")
     ratio = flex.fwd_p95_ms / ours.fwd_p95_ms
     noisy = any(r.fwd_p95_ms / r.fwd_p50_ms > 2 for r in (ours, flex))
     e_o, e_f = ours.max_abs_err_vs_fp64, flex.max_abs_err_vs_fp64
@@ -260,9 +261,11 @@ def run_benchmark(cfg: HarnessConfig, csv_path: Optional[Path] = None,
     fwd_fns = _methods(q_f, k_f, v_f, mask, cfg)
     bwd_fns = _methods(q_g, k_g, v_g, mask, cfg)
     results: List[BenchResult] = []
+    failures: Dict[str, str] = {}
     for label, f_fwd in fwd_fns.items():
         if f_fwd is None:
             print(f"[skip] {label}: not applicable at this shape / unavailable", flush=True)
+            failures[label] = "not applicable at this shape / unavailable"
             continue
         print(f"[run ] {label}: fwd", flush=True)
         try:
@@ -270,10 +273,13 @@ def run_benchmark(cfg: HarnessConfig, csv_path: Optional[Path] = None,
                 lat, peak = _time(f_fwd, cfg.warmup_iters, cfg.measure_iters)
         except torch.cuda.OutOfMemoryError:
             print(f"[OOM ] {label}", flush=True)
+            failures[label] = "out of memory"
             torch.cuda.empty_cache()
             continue
         except Exception as e:  # noqa: BLE001
-            print(f"[fail] {label}: {type(e).__name__}: {e}", flush=True)
+            msg = f"{type(e).__name__}: {str(e).splitlines()[0][:300] if str(e) else ''}"
+            print(f"[fail] {label}: {msg}", flush=True)
+            failures[label] = msg
             continue
         p50_b = p95_b = None
         f_bwd = bwd_fns.get(label)
@@ -305,7 +311,8 @@ def run_benchmark(cfg: HarnessConfig, csv_path: Optional[Path] = None,
         print("  ".join(c.ljust(w) for c, w in zip(r.row(), widths)))
     by = {r.label: r for r in results}
     if OURS in by:
-        print(f"[verdict] {verdict(by[OURS], by.get('flex-attention'))}", flush=True)
+        print(f"[verdict] {verdict(by[OURS], by.get('flex-attention'), failures.get('flex-attention'))}",
+              flush=True)
     if csv_path is not None:
         with open(csv_path, "w", newline="") as f:
             w = csv.writer(f)

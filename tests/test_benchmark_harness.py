@@ -32,6 +32,7 @@ def test_verdict_rules():
     # faster but noisy (p95 / p50 > 2): tie
     assert bm.verdict(_res(bm.OURS, 0.2, 0.5, 1e-3), flex).startswith("TIE")
     assert "no verdict" in bm.verdict(_res(bm.OURS, 1, 1, None), None)
+    assert bm.verdict(_res(bm.OURS, 1, 1, None), None, "boom").endswith("no verdict (boom)")
 
 
 def test_error_shape_is_scaled_down():
