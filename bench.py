@@ -266,8 +266,8 @@ def section_c4(steps: int, warmup: int, cpu_sample: Optional[dict] = None) -> di
     log(f"[c4] decode step after evicting the memory-side cache: {cold * 1e3:.2f} us, "
         f"{res['cold_cache']['kv_gbs']:.0f} GB/s ({100 * res['cold_cache']['frac']:.1f}% of HBM peak)")
     res["rolling_cache"] = _rolling_c4(q, k, v, S, W, fn(), exact_bytes, steps, warmup)
-    if cpu_sample is not None:      # batch 0's 32 heads: (b, h) slices for the CPU leg
-        cpu_sample["c4"] = (q[:1].cpu(), k[:1].cpu(), v[:1].cpu(), mask.cpu())
+    if cpu_sample is not None:      # the whole step for the CPU leg (13 GB of bf16 K / V on the host)
+        cpu_sample["c4"] = (q.cpu(), k.cpu(), v.cpu(), mask.cpu())
     del k, v
     res["gqa"] = _gqa_c4(B, H, NKV, D, S, W, mask, steps, warmup)
     res["multi_query"] = _gqa_c4(B, H, NKV, D, S, W, mask, steps, warmup, H_kv=1)
@@ -430,7 +430,8 @@ def cpu_baseline(cpu_inputs, kept: int, budget_s: float, extra: Optional[dict] =
     share of the budget is spent; sums over slices, extrapolation stated):
     config 2 forward (``value``, kept-block TFLOP/s), and from ``extra``
     config 3 forward + backward (autograd; 14 * BM * BN * D per kept tile)
-    and config 4 decode steps (token-exact kept K/V GB/s)."""
+    and the config 4 decode step (token-exact kept K/V GB/s); config 1
+    forward + backward runs directly (no GPU input needed)."""
     import torch
 
     from oracle.eager_cpu import eager_masked_attention
@@ -480,20 +481,40 @@ def cpu_baseline(cpu_inputs, kept: int, budget_s: float, extra: Optional[dict] =
 
     if "c4" in extra:
         q4, k4, v4, m4 = extra["c4"]
-        H4, N4, D4 = q4.shape[1], k4.shape[2], q4.shape[-1]
+        B4, H4, D4 = q4.shape[0], q4.shape[1], q4.shape[-1]
 
-        def c4_head(h):
-            sl = (slice(0, 1), slice(h, h + 1))
+        def c4_head(i):
+            sl = (slice(i // H4, i // H4 + 1), slice(i % H4, i % H4 + 1))
             eager_masked_attention(q4[sl].float(), k4[sl].float(), v4[sl].float(), m4, 1, 64, True,
                                    4, 2048)
 
-        n4, t4 = _heads_within(share, H4, c4_head)
+        n4, t4 = _heads_within(max(share, 60.0), B4 * H4, c4_head)
         kv = (4 + 2048) * D4 * 2 * 2 * n4
         out["c4"] = {"value": round(kv / t4 / 1e9, 4), "unit": "GB/s",
-                     "sample": (f"config 4 decode, {n4} of 256 (b, h) slices (n_q 1, KV 100000, "
-                                f"D128; the eager path reads all 100000 keys), {t4:.2f} s; "
-                                f"token-exact kept K/V bytes {kv} over that time")}
+                     "sample": (f"config 4 decode step, {n4} of {B4 * H4} (b, h) slices (n_q 1, KV "
+                                f"100000, D128, bf16 cast to fp32 per slice; the eager path reads "
+                                f"all 100000 keys), {t4:.2f} s; token-exact kept K/V bytes {kv} "
+                                f"over that time")}
         log(f"[cpu] c4 decode: {n4} (b, h) slice(s) in {t4:.2f} s, {out['c4']['value']:.3f} GB/s")
+
+    # config 1 runs directly: B1 H4 N1024 D64 fp32 (seed 0), forward + backward
+    g1 = torch.Generator().manual_seed(0)
+    q1, k1, v1 = (torch.randn(1, 4, 1024, 64, generator=g1).requires_grad_(True) for _ in range(3))
+    do1 = torch.randn(1, 4, 1024, 64, generator=torch.Generator().manual_seed(1))
+    from oracle import streaming_oracle as so
+    m1 = torch.from_numpy(so.block_mask(1024, 1024, 4, 256, 64, 64))
+
+    def c1_step(_):
+        for t in (q1, k1, v1):
+            t.grad = None
+        eager_masked_attention(q1, k1, v1, m1, 64, 64, True, 4, 256).backward(do1)
+
+    n1, t1 = _heads_within(min(share, 2.0), 1 << 30, c1_step)
+    f1 = 14.0 * 64 * 64 * 64 * int(m1.sum()) * 4 * n1
+    out["c1"] = {"value": round(f1 / t1 / 1e12, 6), "unit": "TFLOP/s", "ms_per_step": 1e3 * t1 / n1,
+                 "sample": (f"config 1 forward + backward (B1 H4 N1024 D64 fp32, S4 W256), {n1} "
+                            f"steps in {t1:.2f} s")}
+    log(f"[cpu] c1 fwd+bwd: {1e3 * t1 / n1:.2f} ms per step")
     return out
 
 

@@ -107,3 +107,4 @@ def test_cpu_baseline_leg_on_a_small_sample():
     assert out["c3"]["unit"] == "TFLOP/s" and out["c3"]["value"] > 0
     assert "of 2 (b, h) slices" in out["c3"]["sample"]
     assert out["c4"]["unit"] == "GB/s" and out["c4"]["value"] > 0
+    assert out["c1"]["unit"] == "TFLOP/s" and out["c1"]["value"] > 0
