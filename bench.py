@@ -130,7 +130,7 @@ def _traffic(*keys: str):
     """HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE (scaled
     by a plain copy of known size), summed over the named kernels; from
     profiles/hbm_traffic.json, which the profiling commands in
-    profiles/hbm_traffic_c2_c3_c4.md produce. None when not profiled."""
+    profiles/hbm_traffic_c2_c3_c4_c5.md produce. None when not profiled."""
     path = ROOT / "profiles" / "hbm_traffic.json"
     try:
         table = json.loads(path.read_text())["kernels"]
@@ -376,7 +376,8 @@ def section_c5(steps: int, warmup: int) -> dict:
         "fwdbwd_tflops": (f_fwd + f_bwd) / ((fwd + bwd) * 1e-3) / 1e12,
         "attention_ms_12_layers": 12 * (fwd + bwd),
     }
-    res["roofline"] = _roofline(res["fwdbwd_tflops"], PEAK_MFMA_16, "TFLOP/s", "mfma")
+    res["roofline"] = _roofline(res["fwdbwd_tflops"], PEAK_MFMA_16, "TFLOP/s", "mfma",
+                                _traffic("c5_fwd", "c5_dkdv", "c5_dq"))
     log(f"[c5] layer fwd {fwd:.3f} ms, bwd {bwd:.3f} ms ({res['fwdbwd_tflops']:.1f} TF/s)")
     return res
 

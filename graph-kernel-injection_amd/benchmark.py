@@ -226,6 +226,19 @@ def measure_errors(cfg: HarnessConfig) -> Dict[str, Optional[float]]:
     return errors
 
 
+def failure_text(e: BaseException) -> str:
+    """One line naming a failed method's exception: its first line and, for a
+    wrapped error (an Inductor subprocess failure, say), its last non-empty line,
+    where the underlying cause is printed."""
+    lines = [ln.strip() for ln in str(e).splitlines() if ln.strip()]
+    if not lines:
+        return type(e).__name__
+    text = lines[0][:200]
+    if len(lines) > 1 and lines[-1] != lines[0]:
+        text += " ... " + lines[-1][:200]
+    return f"{type(e).__name__}: {text}"
+
+
 def verdict(ours: BenchResult, flex: Optional[BenchResult], flex_error: Optional[str] = None) -> str:
     """Win / tie / loss against FlexAttention (docs/eval_plan.md §5); without a
     FlexAttention result, "no verdict" and why (``flex_error``)."""
@@ -277,7 +290,7 @@ def run_benchmark(cfg: HarnessConfig, csv_path: Optional[Path] = None,
             torch.cuda.empty_cache()
             continue
         except Exception as e:  # noqa: BLE001
-            msg = f"{type(e).__name__}: {str(e).splitlines()[0][:300] if str(e) else ''}"
+            msg = failure_text(e)
             print(f"[fail] {label}: {msg}", flush=True)
             failures[label] = msg
             continue

@@ -182,6 +182,9 @@ __device__ inline uint4 lds_row8(const uint16_t* tile, int row, int col) {
 
 // Stage a 64-row tile of a row-major [n, D] 16-bit matrix: each thread moves
 // P 16-byte chunks, consecutive threads covering consecutive bytes of a row.
+// The loads go through a buffer resource over the rows that exist, so rows at
+// or past n_rows read as zero without a per-element predicate, and the lane
+// offsets are 32-bit (chunk c of the tile sits at byte 16 c).
 template <int D>
 struct RowTile {
   static constexpr int CPR = D / 8;          // 16-byte chunks per row
@@ -189,20 +192,15 @@ struct RowTile {
   static constexpr int P = (CH + 255) / 256;
   uint4 reg[P];
   __device__ inline void load(const uint16_t* base, int r0, int n_rows, int tid) {
-    if (CH % 256 == 0 && r0 + 64 <= n_rows) {   // interior tile: no predicates
-#pragma unroll
-      for (int p = 0; p < P; ++p) {
-        const int c = tid + 256 * p;
-        reg[p] = *(const uint4*)(base + (size_t)(r0 + c / CPR) * D + (c % CPR) * 8);
-      }
-      return;
-    }
+    const int rows = max(0, min(64, n_rows - r0));
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(base + (size_t)r0 * D), (short)0, rows * D * 2, 0x00020000);
 #pragma unroll
     for (int p = 0; p < P; ++p) {
       const int c = tid + 256 * p;
-      const int r = c / CPR, ch = c - r * CPR;
-      reg[p] = (c < CH && r0 + r < n_rows) ? *(const uint4*)(base + (size_t)(r0 + r) * D + ch * 8)
-                                           : make_uint4(0, 0, 0, 0);
+      reg[p] = make_uint4(0, 0, 0, 0);
+      if (CH % 256 == 0 || c < CH)
+        reg[p] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, 16 * c, 0, 0));
     }
   }
   __device__ inline void store(uint16_t* lds, int tid) const {
@@ -229,6 +227,26 @@ __device__ inline uint32_t lds_addr(const void* p) {
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ inline void dma_load16(const void* src, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds)
+               : "memory", "m0");
+}
+// Buffer-resource variant: lane i fetches 16 bytes at the resource base +
+// voff[i] (same LDS placement), so the per-tile address arithmetic is scalar
+// (the base) and the lane offsets stay in registers unchanged; offsets at or
+// past `bytes` read zero instead of faulting. Measured faster than the global
+// form for the forward's K / V tiles.
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+__device__ inline i32x4 buffer_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)(uintptr_t)base;
+  i32x4 r;
+  r.x = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  r.y = __builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));   // stride 0
+  r.z = __builtin_amdgcn_readfirstlane((int)bytes);                   // num_records
+  r.w = 0x00020000;                                                   // DATA_FORMAT 32
+  return r;
+}
+__device__ inline void dma_buf16(i32x4 rsrc, int voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc),
+               "s"(lds)
                : "memory", "m0");
 }
 // 4-byte variant: lane i writes lds + 4 i.
@@ -266,13 +284,15 @@ struct DmaTile {
       off[p] = row * D + ((pch ^ lds_swz<D>(row)) << 3);
     }
   }
+  // Rows r0 .. r0+63 of `base` through a buffer resource over those rows: the
+  // tile base is uniform, so a tile costs no per-lane address arithmetic.
   __device__ inline void load(const uint16_t* base, int r0, const uint16_t* lds) const {
-    const uint16_t* src = base + (size_t)r0 * D;
+    const i32x4 rsrc = buffer_rsrc(base + (size_t)r0 * D, 64 * D * 2);
     const uint32_t l0 = lds_addr(lds);
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
       const int blk = 4 * p + wave;
-      if (NB % 4 == 0 || blk < NB) dma_load16(src + off[p], l0 + blk * 1024);
+      if (NB % 4 == 0 || blk < NB) dma_buf16(rsrc, 2 * off[p], l0 + blk * 1024);
     }
   }
 };
@@ -408,10 +428,10 @@ __host__ __device__ inline uint64_t row_valid_bits(const Geom& g, int q_row, int
          (bit_range(qa - word_window(g) + 1, 63) | bit_range(0, g.sink - 1 - k0));
   }
   if (partial) {                                 // kept blocks of the row's block row
-    const int32_t* mrow = g.mask + (size_t)(q_row / g.bm) * g.n_kb;
+    const int mrow = (q_row / g.bm) * g.n_kb;     // 32-bit: the mask has < 2^31 blocks
     uint64_t kept = 0;
     for (int kb = k0 / g.bn; kb < g.n_kb && kb * g.bn < k0 + 64; ++kb)
-      if (mrow[kb]) kept |= bit_range(kb * g.bn - k0, (kb + 1) * g.bn - 1 - k0);
+      if (g.mask[mrow + kb]) kept |= bit_range(kb * g.bn - k0, (kb + 1) * g.bn - 1 - k0);
     b &= kept;
   }
   return b;
@@ -430,7 +450,7 @@ __host__ __device__ inline uint64_t col_valid_bits(const Geom& g, int kv, int q0
     const int kb = kv / g.bn;
     uint64_t kept = 0;
     for (int qb = q0 / g.bm; qb < g.n_qb && qb * g.bm < q0 + 64; ++qb)
-      if (g.mask[(size_t)qb * g.n_kb + kb]) kept |= bit_range(qb * g.bm - q0, (qb + 1) * g.bm - 1 - q0);
+      if (g.mask[qb * g.n_kb + kb]) kept |= bit_range(qb * g.bm - q0, (qb + 1) * g.bm - 1 - q0);
     b &= kept;
   }
   return b;

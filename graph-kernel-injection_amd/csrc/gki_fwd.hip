@@ -39,15 +39,12 @@ namespace {
 // any reference max.
 constexpr float kRescaleSlack = 8.f;
 
-#ifndef GKI_FWD_MINB128
-#define GKI_FWD_MINB128 2
-#endif
 // Workgroups per CU the compiler must fit in registers: 4 (up to 128 VGPRs) for
 // head_dim <= 64, whose 32 KB of K / V buffers allow four workgroups per CU (the
-// extra waves hide more latency: c3 / c5 forward 4-7% faster than at 3); 2 for
+// extra waves hide more latency: 4-7% faster than three at head_dim 64); 2 for
 // head_dim 128 (64 KB of buffers).
 template <typename T, int D>
-__global__ __launch_bounds__(256, D <= 64 ? 4 : GKI_FWD_MINB128) void fwd_kernel_16(
+__global__ __launch_bounds__(256, D <= 64 ? 4 : 2) void fwd_kernel_16(
     Geom g, const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const uint16_t* __restrict__ V, uint16_t* __restrict__ O, float* __restrict__ LSE,
     const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ row_idx, int n_qt) {

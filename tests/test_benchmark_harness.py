@@ -41,3 +41,11 @@ def test_error_shape_is_scaled_down():
     s = bm._error_shape(cfg)
     assert (s.batch, s.heads, s.seq_len_q, s.seq_len_kv, s.head_dim) == (1, 2, 1, 256, 64)
     assert (s.block_m, s.block_n, s.window_size, s.sink_size) == (1, 64, 128, 4)
+
+
+def test_failure_text_keeps_first_and_last_line():
+    e = RuntimeError("SubprocException: An exception occurred in a subprocess:\n\nTraceback:\n  x\nValueError: bad tile")
+    assert bm.failure_text(e) == ("RuntimeError: SubprocException: An exception occurred in a subprocess: ... "
+                                  "ValueError: bad tile")
+    assert bm.failure_text(RuntimeError("one line")) == "RuntimeError: one line"
+    assert bm.failure_text(RuntimeError()) == "RuntimeError"
