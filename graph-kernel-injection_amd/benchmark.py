@@ -228,14 +228,16 @@ def measure_errors(cfg: HarnessConfig) -> Dict[str, Optional[float]]:
 
 def failure_text(e: BaseException) -> str:
     """One line naming a failed method's exception: its first line and, for a
-    wrapped error (an Inductor subprocess failure, say), its last non-empty line,
-    where the underlying cause is printed."""
+    wrapped error (an Inductor subprocess failure, say), the last line that
+    names an error, where the underlying cause is printed (generic hints such
+    as "Set TORCHDYNAMO_VERBOSE=1 ..." are skipped)."""
     lines = [ln.strip() for ln in str(e).splitlines() if ln.strip()]
     if not lines:
         return type(e).__name__
     text = lines[0][:200]
-    if len(lines) > 1 and lines[-1] != lines[0]:
-        text += " ... " + lines[-1][:200]
+    causes = [ln for ln in lines[1:] if ("Error" in ln or "error:" in ln) and not ln.startswith("Set ")]
+    if causes and causes[-1] != lines[0]:
+        text += " ... " + causes[-1][:200]
     return f"{type(e).__name__}: {text}"
 
 
@@ -292,6 +294,8 @@ def run_benchmark(cfg: HarnessConfig, csv_path: Optional[Path] = None,
         except Exception as e:  # noqa: BLE001
             msg = failure_text(e)
             print(f"[fail] {label}: {msg}", flush=True)
+            for ln in str(e).splitlines()[-12:]:
+                print(f"[fail-detail] {ln}", flush=True)
             failures[label] = msg
             continue
         p50_b = p95_b = None

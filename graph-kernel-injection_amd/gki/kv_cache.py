@@ -31,8 +31,7 @@ import torch
 
 from . import _lib
 from .masks import StreamingMaskSpec
-from .ops import (_DTYPE_CODE, _aligned, _current_stream, _decode_on_mfma, _decode_slots,
-                  _decode_splits, _on_device)
+from .ops import _DTYPE_CODE, _aligned, _current_stream, _decode_plan, _on_device
 
 _DECODE_HEAD_DIMS = (64, 128)
 
@@ -150,28 +149,25 @@ class StreamingKVCache:
         _, _, n_tokens = rolling_stream(self.length, n_q, self.sink_size, self.window_size,
                                         self.ring_size)
         B, H, H_kv = self.batch, int(q.shape[1]), self.heads
-        ts = _lib.tile_sizes()
-        mfma = _decode_on_mfma(_DTYPE_CODE[self.dtype], self.head_dim, H // H_kv, n_q,
-                               ts["decode_tile_m"])
-        n_splits = _decode_splits(n_tokens, _decode_slots(B, H, H_kv, n_q, ts["decode_max_q"], mfma))
-        o = torch.empty_like(q)
-        lse = torch.empty((B, H, n_q), dtype=torch.float32, device=self.device)
         lib = _lib.load()
+        dtype = _DTYPE_CODE[self.dtype]
+        _, n_splits, ws_floats = _decode_plan(lib, dtype, B, H, H_kv, n_q, self.head_dim, n_tokens, True)
+        o = torch.empty_like(q)
+        # the LSE rows (padded to 256 bytes), then the split workspace: one allocation
+        pad = (B * H * n_q + 63) & ~63
+        scratch = torch.empty(pad + ws_floats, dtype=torch.float32, device=self.device)
         with _on_device(self.device):
             stream = _current_stream(self.device)
-            ws_ptr = 0
-            if n_splits > 1:
-                ws = torch.empty(int(lib.gki_bsa_decode_workspace_floats(B, H, n_q, self.head_dim,
-                                                                         n_splits)),
-                                 dtype=torch.float32, device=self.device)
-                ws_ptr = ws.data_ptr()
             _lib.check(lib.gki_rolling_decode(
                 q.data_ptr(), self.k_cache.data_ptr(), self.v_cache.data_ptr(), o.data_ptr(),
-                lse.data_ptr(), _DTYPE_CODE[self.dtype], B, H, H_kv, n_q, self.head_dim, self.sink_size,
-                self.window_size, self.ring_size, self.length, float(softmax_scale), ws_ptr,
-                n_splits, stream), "gki_rolling_decode")
+                scratch.data_ptr(), dtype, B, H, H_kv, n_q, self.head_dim, self.sink_size,
+                self.window_size, self.ring_size, self.length, float(softmax_scale),
+                scratch.data_ptr() + 4 * pad if ws_floats else 0, n_splits, stream),
+                "gki_rolling_decode")
+        if not return_lse:
+            return o
         # the kernels store the LSE in base 2; the API returns natural-log units
-        return (o, lse.mul_(math.log(2.0))) if return_lse else o
+        return o, scratch[:B * H * n_q].view(B, H, n_q).mul(math.log(2.0))
 
     def step(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
              softmax_scale: Optional[float] = None) -> torch.Tensor:

@@ -92,11 +92,31 @@ def _decode_slots(B: int, H: int, H_kv: int, n_q: int, max_q: int, mfma: bool = 
     return B * H // gq
 
 
+# decode launch plans: (dtype, B, H, H_kv, n_q, D, n_tokens, computed stream) ->
+# (on the matrix cores, splits, split workspace floats); a few entries per model
+_DECODE_PLANS: dict = {}
+
+
+def _decode_plan(lib, dtype: int, B: int, H: int, H_kv: int, N_Q: int, D: int, n_tokens: int,
+                 ring: bool) -> Tuple[bool, int, int]:
+    key = (dtype, B, H, H_kv, N_Q, D, n_tokens, ring)
+    plan = _DECODE_PLANS.get(key)
+    if plan is None:
+        ts = _lib.tile_sizes()
+        mfma = ring and _decode_on_mfma(dtype, D, H // H_kv, N_Q, ts["decode_tile_m"])
+        n_splits = _decode_splits(n_tokens, _decode_slots(B, H, H_kv, N_Q, ts["decode_max_q"], mfma))
+        ws = int(lib.gki_bsa_decode_workspace_floats(B, H, N_Q, D, n_splits)) if n_splits > 1 else 0
+        plan = _DECODE_PLANS[key] = (mfma, n_splits, ws)
+    return plan
+
+
 def _attention_forward(q, k, v, block_mask, softmax_scale, block_m, block_n, is_causal, sink_size,
-                       window_size, enable_gqa):
+                       window_size, enable_gqa, need_lse=True):
     """Validation and the forward launch (``sparse_triton_kernel.py:615-682``):
     returns (o, lse, q, k, v, block_mask, q_offset) with q / k / v / block_mask
-    as the kernels read them (16-byte aligned, int32 mask on q's device)."""
+    as the kernels read them (16-byte aligned, int32 mask on q's device).
+    Without ``need_lse`` (inference) a decode step keeps its LSE and split
+    workspace in one scratch allocation and returns lse None."""
     lib = _lib.load()
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
         raise ValueError("Q/K/V must be 4-D [B, H, N, D] tensors")
@@ -131,7 +151,7 @@ def _attention_forward(q, k, v, block_mask, softmax_scale, block_m, block_n, is_
     block_mask = _device_mask(block_mask, dev)
 
     o = torch.empty_like(q)
-    lse = torch.empty((B, H, N_Q), dtype=torch.float32, device=dev)
+    lse = None
     q_offset = N_KV - N_Q
     dtype = _DTYPE_CODE[q.dtype]
     common = (block_mask.data_ptr(), n_qb, n_kb, block_m, block_n, float(softmax_scale),
@@ -143,28 +163,36 @@ def _attention_forward(q, k, v, block_mask, softmax_scale, block_m, block_n, is_
         if N_Q <= ts["decode_max_q"] and D in _DECODE_HEAD_DIMS:
             sched = decode_schedule(block_mask, N_Q, N_KV, block_m, block_n, bool(is_causal),
                                     int(sink_size), int(window_size))
-            mfma = bool(sched.ring) and _decode_on_mfma(dtype, D, H // H_kv, N_Q,
-                                                        ts["decode_tile_m"])
-            n_splits = _decode_splits(sched.n_tokens,
-                                      _decode_slots(B, H, H_kv, N_Q, ts["decode_max_q"], mfma))
-            ws_ptr = 0
-            if n_splits > 1:
-                ws = torch.empty(int(lib.gki_bsa_decode_workspace_floats(B, H, N_Q, D, n_splits)),
-                                 dtype=torch.float32, device=dev)
-                ws_ptr = ws.data_ptr()
+            _, n_splits, ws_floats = _decode_plan(lib, dtype, B, H, H_kv, N_Q, D, sched.n_tokens,
+                                                  bool(sched.ring))
+            n_lse = B * H * N_Q
+            if need_lse:
+                lse = torch.empty((B, H, N_Q), dtype=torch.float32, device=dev)
+                lse_ptr = lse.data_ptr()
+                ws_ptr = 0
+                if ws_floats:
+                    ws = torch.empty(ws_floats, dtype=torch.float32, device=dev)
+                    ws_ptr = ws.data_ptr()
+            else:
+                # one allocation: the LSE rows (padded to 256 bytes), then the workspace
+                pad = (n_lse + 63) & ~63
+                scratch = torch.empty(pad + ws_floats, dtype=torch.float32, device=dev)
+                lse_ptr = scratch.data_ptr()
+                ws_ptr = lse_ptr + 4 * pad if ws_floats else 0
             if sched.ring:
                 # the stream is the StreamingLLM one: positions computed in
                 # the kernel (no list read), same stream and arithmetic
                 _lib.check(lib.gki_rolling_decode(
-                    q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                    q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse_ptr,
                     dtype, B, H, H_kv, N_Q, D, int(sink_size), int(window_size), sched.ring,
                     N_KV, float(softmax_scale), ws_ptr, n_splits, stream), "gki_rolling_decode")
             else:
                 _lib.check(lib.gki_bsa_decode(
-                    q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), dtype,
+                    q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse_ptr, dtype,
                     B, H, H_kv, N_Q, N_KV, D, sched.tokens.data_ptr(), sched.n_tokens, *common,
                     ws_ptr, n_splits, stream), "gki_bsa_decode")
         else:
+            lse = torch.empty((B, H, N_Q), dtype=torch.float32, device=dev)
             sched = fwd_schedule(block_mask, N_Q, N_KV, block_m, block_n, bool(is_causal),
                                  int(sink_size), int(window_size), q.dtype == torch.float32)
             _lib.check(lib.gki_bsa_fwd(
@@ -281,7 +309,7 @@ def block_sparse_attention(
     if not (torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad)):
         # nothing to differentiate (inference, a decode step): the same forward
         # without the autograd node and its saved tensors
-        return _attention_forward(*args, enable_gqa)[0]
+        return _attention_forward(*args, enable_gqa, need_lse=False)[0]
     if enable_gqa:
         args += (True,)
     return _BlockSparseFlashAttention.apply(*args)

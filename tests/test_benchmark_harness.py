@@ -43,9 +43,11 @@ def test_error_shape_is_scaled_down():
     assert (s.block_m, s.block_n, s.window_size, s.sink_size) == (1, 64, 128, 4)
 
 
-def test_failure_text_keeps_first_and_last_line():
-    e = RuntimeError("SubprocException: An exception occurred in a subprocess:\n\nTraceback:\n  x\nValueError: bad tile")
+def test_failure_text_keeps_first_line_and_the_cause():
+    e = RuntimeError("SubprocException: An exception occurred in a subprocess:\n\nTraceback:\n  x\n"
+                     "ValueError: bad tile\n\nSet TORCHDYNAMO_VERBOSE=1 for the internal stack trace")
     assert bm.failure_text(e) == ("RuntimeError: SubprocException: An exception occurred in a subprocess: ... "
                                   "ValueError: bad tile")
     assert bm.failure_text(RuntimeError("one line")) == "RuntimeError: one line"
+    assert bm.failure_text(RuntimeError("first\nno cause here")) == "RuntimeError: first"
     assert bm.failure_text(RuntimeError()) == "RuntimeError"

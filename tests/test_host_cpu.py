@@ -151,6 +151,32 @@ def test_decode_routing_rules():
     assert ops._decode_splits(2052, 8) == 8 and ops._decode_splits(100, 1) == 1
 
 
+def test_decode_plan_is_memoized_and_matches_the_rules(monkeypatch):
+    """The per-call decode plan (matrix cores?, splits, workspace floats) equals
+    the rules above plus the library's workspace size, and a second call with
+    the same key asks the library nothing."""
+    from gki import ops
+
+    lib = _lib.load()
+    ops._DECODE_PLANS.clear()
+    ts = _lib.tile_sizes()
+    for (dt, B, H, H_kv, n_q, D, n_tok, ring) in [(2, 8, 32, 8, 1, 128, 2052, True),
+                                                  (2, 8, 32, 32, 1, 128, 2052, True),
+                                                  (2, 8, 32, 1, 1, 128, 2052, True),
+                                                  (1, 1, 4, 4, 4, 64, 600, False),
+                                                  (0, 2, 8, 8, 1, 64, 5000, True)]:
+        mfma = ring and ops._decode_on_mfma(dt, D, H // H_kv, n_q, ts["decode_tile_m"])
+        splits = ops._decode_splits(n_tok, ops._decode_slots(B, H, H_kv, n_q, ts["decode_max_q"], mfma))
+        ws = int(lib.gki_bsa_decode_workspace_floats(B, H, n_q, D, splits)) if splits > 1 else 0
+        assert ops._decode_plan(lib, dt, B, H, H_kv, n_q, D, n_tok, ring) == (mfma, splits, ws)
+
+    class _NoLib:
+        def __getattr__(self, name):
+            raise AssertionError("memoized plan must not call the library")
+
+    assert ops._decode_plan(_NoLib(), 2, 8, 32, 8, 1, 128, 2052, True)[1] == 4
+
+
 def test_dkdv_work_list_rejects_bad_columns():
     lib = _lib.load()
     out = [ctypes.c_int32() for _ in range(3)]
