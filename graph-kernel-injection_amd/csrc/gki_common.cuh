@@ -185,11 +185,11 @@ __device__ inline uint4 lds_row8(const uint16_t* tile, int row, int col) {
 // The loads go through a buffer resource over the rows that exist, so rows at
 // or past n_rows read as zero without a per-element predicate, and the lane
 // offsets are 32-bit (chunk c of the tile sits at byte 16 c).
-template <int D>
+template <int D, int NT = 256>
 struct RowTile {
   static constexpr int CPR = D / 8;          // 16-byte chunks per row
   static constexpr int CH = 64 * CPR;
-  static constexpr int P = (CH + 255) / 256;
+  static constexpr int P = (CH + NT - 1) / NT;
   uint4 reg[P];
   __device__ inline void load(const uint16_t* base, int r0, int n_rows, int tid) {
     const int rows = max(0, min(64, n_rows - r0));
@@ -197,16 +197,16 @@ struct RowTile {
         (void*)(base + (size_t)r0 * D), (short)0, rows * D * 2, 0x00020000);
 #pragma unroll
     for (int p = 0; p < P; ++p) {
-      const int c = tid + 256 * p;
+      const int c = tid + NT * p;
       reg[p] = make_uint4(0, 0, 0, 0);
-      if (CH % 256 == 0 || c < CH)
+      if (CH % NT == 0 || c < CH)
         reg[p] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, 16 * c, 0, 0));
     }
   }
   __device__ inline void store(uint16_t* lds, int tid) const {
 #pragma unroll
     for (int p = 0; p < P; ++p) {
-      const int c = tid + 256 * p;
+      const int c = tid + NT * p;
       if (c < CH) *(uint4*)(lds + lds_off<D>(c / CPR, (c % CPR) * 8)) = reg[p];
     }
   }
@@ -265,13 +265,14 @@ __device__ inline void dma_wait() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 // the swizzled LDS layout with LDS-DMA loads: no VGPR staging and no ds_write.
 // One wave instruction fills 1 KB of LDS, lane i writing bytes 16i..16i+15,
 // so the swizzle is applied on the global side: lane i fetches the chunk that
-// belongs at its LDS position. The 256 threads cover the tile's D/8 blocks of
-// 1 KB; `off` is the lane's element offset inside the tile for each block it
-// moves (computed once). Only for tiles whose 64 rows are all in bounds.
-template <int D>
+// belongs at its LDS position. The workgroup's NW waves cover the tile's D/8
+// blocks of 1 KB (block NW p + wave for p = 0, 1, ...); `off` is the lane's
+// element offset inside the tile for each block it moves (computed once).
+// Only for tiles whose 64 rows are all in bounds.
+template <int D, int NW = 4>
 struct DmaTile {
   static constexpr int NB = D / 8;                     // 1 KB blocks per tile
-  static constexpr int NP = (NB + 3) / 4;              // blocks per wave
+  static constexpr int NP = (NB + NW - 1) / NW;        // blocks per wave
   int off[NP];
   int wave;
   __device__ inline void init(int tid) {
@@ -279,7 +280,7 @@ struct DmaTile {
     const int lane = tid & 63;
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
-      const int e = (4 * p + wave) * 512 + 8 * lane;   // LDS element offset
+      const int e = (NW * p + wave) * 512 + 8 * lane;  // LDS element offset
       const int row = e / D, pch = (e % D) >> 3;
       off[p] = row * D + ((pch ^ lds_swz<D>(row)) << 3);
     }
@@ -291,8 +292,8 @@ struct DmaTile {
     const uint32_t l0 = lds_addr(lds);
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
-      const int blk = 4 * p + wave;
-      if (NB % 4 == 0 || blk < NB) dma_buf16(rsrc, 2 * off[p], l0 + blk * 1024);
+      const int blk = NW * p + wave;
+      if (NB % NW == 0 || blk < NB) dma_buf16(rsrc, 2 * off[p], l0 + blk * 1024);
     }
   }
 };

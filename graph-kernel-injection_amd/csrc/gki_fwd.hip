@@ -39,17 +39,26 @@ namespace {
 // any reference max.
 constexpr float kRescaleSlack = 8.f;
 
+// Rows per wave: kFwdRB 16-row blocks, every K / V^T operand read feeding
+// kFwdRB MFMAs; 8 / kFwdRB waves per 128-row workgroup. One block per wave
+// (eight waves, twice the waves per SIMD at head_dim 128) was 10% slower: the
+// doubled LDS reads per MFMA cost more than the occupancy gained.
+constexpr int kFwdRB = 2;
+constexpr int kFwdThreads = 64 * (8 / kFwdRB);
 // Workgroups per CU the compiler must fit in registers: 4 (up to 128 VGPRs) for
 // head_dim <= 64, whose 32 KB of K / V buffers allow four workgroups per CU (the
 // extra waves hide more latency: 4-7% faster than three at head_dim 64); 2 for
 // head_dim 128 (64 KB of buffers).
 template <typename T, int D>
-__global__ __launch_bounds__(256, D <= 64 ? 4 : 2) void fwd_kernel_16(
+__global__ __launch_bounds__(kFwdThreads, D <= 64 ? 4 : 2) void fwd_kernel_16(
     Geom g, const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const uint16_t* __restrict__ V, uint16_t* __restrict__ O, float* __restrict__ LSE,
     const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ row_idx, int n_qt) {
   constexpr int KS = (D + 31) / 32;   // k-steps of the QK^T contraction
   constexpr int DT = D / 16;          // 16-row tiles of O^T
+  constexpr int RB = kFwdRB;
+  constexpr int NW = 8 / RB;          // waves per workgroup
+  constexpr int NT = 64 * NW;
   __shared__ __align__(16) uint16_t sk[2][kTileN * D];
   __shared__ __align__(16) uint16_t sv[2][kTileN * D];
 
@@ -60,11 +69,11 @@ __global__ __launch_bounds__(256, D <= 64 ? 4 : 2) void fwd_kernel_16(
   const size_t kb = (size_t)kv_bh(g, bh) * g.n_kv * D;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int grp = lane >> 4, col = lane & 15;
-  const int qw = qt * kTileMF + wave * 32;   // first row of this wave
+  const int qw = qt * kTileMF + wave * 16 * RB;   // first row of this wave
 
-  uint4 qf[2][KS];
+  uint4 qf[RB][KS];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
+  for (int h = 0; h < RB; ++h) {
     const int q = qw + 16 * h + col;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
@@ -74,18 +83,21 @@ __global__ __launch_bounds__(256, D <= 64 ? 4 : 2) void fwd_kernel_16(
     }
   }
 
-  floatx4 o[2][DT];
-#pragma unroll
-  for (int h = 0; h < 2; ++h)
-#pragma unroll
-    for (int i = 0; i < DT; ++i) o[h][i] = floatx4{0.f, 0.f, 0.f, 0.f};
+  floatx4 o[RB][DT];
   // Row sums run on the MFMA pipe (ones x P^T): lane (g, c) holds the sum of
   // row c in every component; it sums the same 16-bit P that multiplies V.
-  floatx4 lsum[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
-  float m[2] = {kNegInf, kNegInf};
+  floatx4 lsum[RB];
+  float m[RB];
+#pragma unroll
+  for (int h = 0; h < RB; ++h) {
+#pragma unroll
+    for (int i = 0; i < DT; ++i) o[h][i] = floatx4{0.f, 0.f, 0.f, 0.f};
+    lsum[h] = floatx4{0.f, 0.f, 0.f, 0.f};
+    m[h] = kNegInf;
+  }
   const uint4 ones = T::ones8();
 
-  DmaTile<D> dma;
+  DmaTile<D, NW> dma;
   dma.init(tid);
   // Full tiles go LDS-DMA; the ragged last kv tile goes through registers so
   // that its out-of-range rows are zero (P = 0 must not meet stale V).
@@ -94,7 +106,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 4 : 2) void fwd_kernel_16(
       dma.load(K + kb, k0, sk[b]);
       dma.load(V + kb, k0, sv[b]);
     } else {
-      RowTile<D> t;
+      RowTile<D, NT> t;
       t.load(K + kb, k0, g.n_kv, tid);
       t.store(sk[b], tid);
       t.load(V + kb, k0, g.n_kv, tid);
@@ -120,22 +132,23 @@ __global__ __launch_bounds__(256, D <= 64 ? 4 : 2) void fwd_kernel_16(
     const uint16_t* ck = sk[buf];
     const uint16_t* cv = sv[buf];
 
-    floatx4 s[2][4];
+    floatx4 s[RB][4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      s[0][t] = s[1][t] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int h = 0; h < RB; ++h) s[h][t] = floatx4{0.f, 0.f, 0.f, 0.f};
       const int r = rho(t, col);
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         const int d0 = 32 * ks + 8 * grp;
         const uint4 a = (d0 < D) ? lds_row8<D>(ck, r, d0) : make_uint4(0, 0, 0, 0);
-        s[0][t] = T::mfma(a, qf[0][ks], s[0][t]);
-        s[1][t] = T::mfma(a, qf[1][ks], s[1][t]);
+#pragma unroll
+        for (int h = 0; h < RB; ++h) s[h][t] = T::mfma(a, qf[h][ks], s[h][t]);
       }
     }
 
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < RB; ++h) {
       const int q0 = qw + 16 * h;
       const bool need_mask = partial || (q0 + 15 >= g.n_q) || (k0 + kTileN > g.n_kv) ||
                              !tile_all_visible(g, q0, min(q0 + 15, g.n_q - 1), k0, k0 + kTileN - 1);
@@ -173,23 +186,24 @@ __global__ __launch_bounds__(256, D <= 64 ? 4 : 2) void fwd_kernel_16(
 
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
-      const uint4 b0 = pack8<T>(s[0][2 * st], s[0][2 * st + 1]);
-      const uint4 b1 = pack8<T>(s[1][2 * st], s[1][2 * st + 1]);
+      uint4 b[RB];
+#pragma unroll
+      for (int h = 0; h < RB; ++h) b[h] = pack8<T>(s[h][2 * st], s[h][2 * st + 1]);
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
         const uint4 a = lds_tr8<D>(cv, 32 * st, 16 * dt, lane);
-        o[0][dt] = T::mfma(a, b0, o[0][dt]);
-        o[1][dt] = T::mfma(a, b1, o[1][dt]);
+#pragma unroll
+        for (int h = 0; h < RB; ++h) o[h][dt] = T::mfma(a, b[h], o[h][dt]);
       }
-      lsum[0] = T::mfma(ones, b0, lsum[0]);
-      lsum[1] = T::mfma(ones, b1, lsum[1]);
+#pragma unroll
+      for (int h = 0; h < RB; ++h) lsum[h] = T::mfma(ones, b[h], lsum[h]);
     }
     dma_wait();        // the next tile's LDS-DMA has landed before the barrier
     __syncthreads();
   }
 
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
+  for (int h = 0; h < RB; ++h) {
     const int my_q = qw + 16 * h + col;
     const float l_tot = lsum[h][0];
     const bool valid = l_tot > 0.f;
@@ -359,11 +373,11 @@ int launch_fwd(int dtype, const Geom& g, const void* q, const void* k, const voi
     hipLaunchKernelGGL(fwd_kernel_32<D>, dim3(grid), dim3(256), 0, stream, g, (const float*)q,
                        (const float*)k, (const float*)v, (float*)o, lse, row_ptr, row_idx, n_qt);
   } else if (dtype == kF16) {
-    hipLaunchKernelGGL((fwd_kernel_16<F16, D>), dim3(grid), dim3(256), 0, stream, g,
+    hipLaunchKernelGGL((fwd_kernel_16<F16, D>), dim3(grid), dim3(kFwdThreads), 0, stream, g,
                        (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, lse,
                        row_ptr, row_idx, n_qt);
   } else {
-    hipLaunchKernelGGL((fwd_kernel_16<BF16, D>), dim3(grid), dim3(256), 0, stream, g,
+    hipLaunchKernelGGL((fwd_kernel_16<BF16, D>), dim3(grid), dim3(kFwdThreads), 0, stream, g,
                        (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, lse,
                        row_ptr, row_idx, n_qt);
   }
