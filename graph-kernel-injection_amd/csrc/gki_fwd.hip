@@ -38,6 +38,11 @@ namespace {
 // rescale is almost never needed. O = acc / l and LSE = m + ln(l) are exact for
 // any reference max.
 constexpr float kRescaleSlack = 8.f;
+// Reference max of a row before it has seen a visible key: the most negative
+// finite float, so exp2(s * c - m) needs no guard (a masked score gives
+// exp2(-inf) = 0) and any visible score, whose scaled value is finite and
+// larger, replaces it at the first rescale test.
+constexpr float kNoMax = -3.40282347e38f;
 
 // Rows per wave: kFwdRB 16-row blocks, every K / V^T operand read feeding
 // kFwdRB MFMAs; 8 / kFwdRB waves per 128-row workgroup. One block per wave
@@ -87,13 +92,18 @@ __global__ __launch_bounds__(kFwdThreads, D <= 64 ? 4 : 2) void fwd_kernel_16(
   // Row sums run on the MFMA pipe (ones x P^T): lane (g, c) holds the sum of
   // row c in every component; it sums the same 16-bit P that multiplies V.
   floatx4 lsum[RB];
-  float m[RB];
+  // m: the row's reference max (scaled, log2 units); thr: the unscaled score
+  // above which it must move, (m + slack) / c, so the per-tile test is one
+  // compare (qk_scale_log2 = c > 0)
+  float m[RB], thr[RB];
+  const float inv_c = __builtin_amdgcn_rcpf(g.qk_scale_log2);   // a trigger: approximate is fine
 #pragma unroll
   for (int h = 0; h < RB; ++h) {
 #pragma unroll
     for (int i = 0; i < DT; ++i) o[h][i] = floatx4{0.f, 0.f, 0.f, 0.f};
     lsum[h] = floatx4{0.f, 0.f, 0.f, 0.f};
-    m[h] = kNegInf;
+    m[h] = kNoMax;
+    thr[h] = (kNoMax + kRescaleSlack) * inv_c;
   }
   const uint4 ones = T::ones8();
 
@@ -166,22 +176,23 @@ __global__ __launch_bounds__(kFwdThreads, D <= 64 ? 4 : 2) void fwd_kernel_16(
         for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[h][t][i]);
       // A row's max exceeds the reference by the slack only if one of its
       // lanes' maxima does (qk_scale_log2 > 0, so scaling after the max is
-      // exact): the cross-lane reduction runs only then.
-      if (__any(mx * g.qk_scale_log2 > m[h] + kRescaleSlack)) {
+      // exact): the cross-lane reduction runs only then. The threshold is a
+      // trigger only: whether m moves is decided exactly inside.
+      if (__any(mx > thr[h])) {
         mx = wave_max16x4(mx) * g.qk_scale_log2;
         const bool grow = mx > m[h] + kRescaleSlack;
         const float alpha = grow ? __builtin_amdgcn_exp2f(m[h] - mx) : 1.f;
         m[h] = grow ? mx : m[h];
+        thr[h] = (m[h] + kRescaleSlack) * inv_c;
         lsum[h][0] *= alpha;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) o[h][dt] *= alpha;
       }
-      const float m_use = (m[h] == kNegInf) ? 0.f : m[h];
 #pragma unroll
       for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          s[h][t][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[h][t][i], g.qk_scale_log2, -m_use));
+          s[h][t][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[h][t][i], g.qk_scale_log2, -m[h]));
     }
 
 #pragma unroll
