@@ -191,10 +191,16 @@ struct RowTile {
   static constexpr int CH = 64 * CPR;
   static constexpr int P = (CH + NT - 1) / NT;
   uint4 reg[P];
+  // base and r0 are uniform at every call site (kernel arguments and a tile
+  // index from the schedule); reading them through readfirstlane lets the
+  // compiler keep the resource in scalar registers (no per-lane loop).
   __device__ inline void load(const uint16_t* base, int r0, int n_rows, int tid) {
     const int rows = max(0, min(64, n_rows - r0));
+    const uint64_t a = (uint64_t)(uintptr_t)(base + (size_t)r0 * D);
+    const uint64_t u = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a) |
+                       ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32)) << 32);
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(base + (size_t)r0 * D), (short)0, rows * D * 2, 0x00020000);
+        (void*)(uintptr_t)u, (short)0, __builtin_amdgcn_readfirstlane(rows * D * 2), 0x00020000);
 #pragma unroll
     for (int p = 0; p < P; ++p) {
       const int c = tid + NT * p;

@@ -102,6 +102,8 @@ def _decode_plan(lib, dtype: int, B: int, H: int, H_kv: int, N_Q: int, D: int, n
     key = (dtype, B, H, H_kv, N_Q, D, n_tokens, ring)
     plan = _DECODE_PLANS.get(key)
     if plan is None:
+        if len(_DECODE_PLANS) >= 4096:      # a growing full cache adds one key per step
+            _DECODE_PLANS.clear()
         ts = _lib.tile_sizes()
         mfma = ring and _decode_on_mfma(dtype, D, H // H_kv, N_Q, ts["decode_tile_m"])
         n_splits = _decode_splits(n_tokens, _decode_slots(B, H, H_kv, N_Q, ts["decode_max_q"], mfma))
