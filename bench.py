@@ -323,15 +323,19 @@ def _rolling_c4(q, k, v, S, W, o_full, exact_bytes, steps, warmup) -> dict:
     k1, v1 = k[:, :, -1:].contiguous(), v[:, :, -1:].contiguous()
     step_avg, _ = _time_calls(lambda: cache.step(q, k1, v1), steps, warmup)
     gbs = exact_bytes / (avg * 1e-3) / 1e9
+    cold = _time_cold(lambda: cache.attend(q))
     cache_bytes = 2 * cache.k_cache.numel() * cache.k_cache.element_size()
     log(f"[c4] rolling cache ({cache.capacity} slots, {cache_bytes / 1e6:.0f} MB vs "
         f"{2 * k.numel() * k.element_size() / 1e9:.2f} GB full): decode {avg * 1e3:.2f} us "
         f"({gbs:.0f} GB/s), append+decode step {step_avg * 1e3:.2f} us, "
-        f"bit-identical to the full-cache decode: {identical}")
+        f"bit-identical to the full-cache decode: {identical}; memory-side cache evicted: "
+        f"{cold * 1e3:.2f} us ({100 * exact_bytes / (cold * 1e-3) / 1e9 / PEAK_HBM:.1f}% of HBM peak)")
     return {"slots": cache.capacity, "cache_bytes": cache_bytes,
             "full_cache_bytes": 2 * k.numel() * k.element_size(), "decode_ms": avg,
             "decode_p50_ms": statistics.median(per), "kv_gbs": gbs, "step_ms": step_avg,
-            "identical_to_full_cache": identical}
+            "identical_to_full_cache": identical,
+            "cold_cache": {"per_call_ms": cold, "kv_gbs": exact_bytes / (cold * 1e-3) / 1e9,
+                           "frac": exact_bytes / (cold * 1e-3) / 1e9 / PEAK_HBM}}
 
 
 def section_c5(steps: int, warmup: int) -> dict:
