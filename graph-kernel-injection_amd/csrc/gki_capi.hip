@@ -85,6 +85,8 @@ int make_geom(Geom& g, int dtype, int B, int H, int H_kv, int n_q, int n_kv, int
   GKI_REQUIRE(block_m > 0 && block_n > 0, 1, "block_m and block_n must be positive");
   GKI_REQUIRE(n_qb == (n_q + block_m - 1) / block_m && n_kb == (n_kv + block_n - 1) / block_n, 1,
               "block mask shape does not match ceil(n_q/block_m) x ceil(n_kv/block_n)");
+  GKI_REQUIRE((int64_t)n_qb * n_kb < (1ll << 31), 1,
+              "block mask too large (the kernels index it with 32-bit offsets)");
   GKI_REQUIRE(sink >= 0 && window >= 0, 1, "sink_size and window_size must be non-negative");
   GKI_REQUIRE(std::isfinite(scale), 1, "softmax_scale must be finite");
   GKI_REQUIRE((int64_t)n_kv < (1ll << kPartialBit), 1, "n_kv too large");

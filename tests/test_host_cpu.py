@@ -234,3 +234,8 @@ def test_capi_rejects_bad_arguments_before_launch():
     rc = lib.gki_bsa_fwd(1, 1, 1, 1, 1, 2, 1, 6, 4, 64, 64, 64, 1, 1, 1, 1, 1, 1, 64, 64, 0.1, 1, 4,
                          8, null)
     assert rc == 1 and b"H_kv" in lib.gki_last_error()
+    # a block mask of 2^31 or more entries (kernels index it with 32-bit offsets)
+    n = 1 << 20
+    rc = lib.gki_bsa_fwd(16, 16, 16, 16, 16, 2, 1, 1, 1, n, n, 64, 16, 16, 1, 16, n // 16, n // 16, 16,
+                         16, 0.1, 1, 4, 8, null)
+    assert rc == 1 and b"block mask too large" in lib.gki_last_error()
