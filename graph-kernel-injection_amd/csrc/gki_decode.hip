@@ -300,11 +300,16 @@ __global__ __launch_bounds__(64 * decode_waves<NQ>()) void decode_kernel(
   const int bhq0 = wgh * gq;                               // first q head of this workgroup
   const size_t qb = (size_t)bhq0 * g.n_q * D;
   const size_t kb = (size_t)kv_bh(g, bhq0) * kv_rows * D;
-  // this workgroup's slice of the token stream, then this wave's contiguous part
+  // this workgroup's slice of the token stream
   const int g0 = (int)(((int64_t)n_tokens * split) / n_splits);
   const int g1 = (int)(((int64_t)n_tokens * (split + 1)) / n_splits);
-  const int w0 = g0 + (int)(((int64_t)(g1 - g0) * wave) / NW);
-  const int w1 = g0 + (int)(((int64_t)(g1 - g0) * (wave + 1)) / NW);
+  // The waves take the slice's rounds of RT tokens in turn (wave w: rounds w,
+  // w + NW, ...), so the workgroup sweeps its K / V rows in address order:
+  // with the memory-side cache cold this reads 2% faster than one contiguous
+  // part per wave (12 concurrent streams per slice), and the same warm.
+  constexpr int ST = NW * RT;
+  const int w0 = g0 + wave * RT;
+  const int w1 = g1;
   const int tk = lane / LPT, ch = lane % LPT;
 
   DecodeQ<T, NQ> qv;
@@ -333,18 +338,18 @@ __global__ __launch_bounds__(64 * decode_waves<NQ>()) void decode_kernel(
     R ra, rb;
     int pa[NU], pb[NU];
     R::positions(src, w0, w1, tk, pa);
-    R::positions(src, w0 + RT, w1, tk, pb);
+    R::positions(src, w0 + ST, w1, tk, pb);
     ra.fetch(src, pa, ch, K, V, kb);
-    for (int t0 = w0; t0 < w1; t0 += 2 * RT) {
-      const bool has_b = t0 + RT < w1;
+    for (int t0 = w0; t0 < w1; t0 += 2 * ST) {
+      const bool has_b = t0 + ST < w1;
       if (has_b) {
-        R::positions(src, t0 + 2 * RT, w1, tk, pa);
+        R::positions(src, t0 + 2 * ST, w1, tk, pa);
         rb.fetch(src, pb, ch, K, V, kb);
       }
       decode_consume<T, D, NQ, NU, EXACT>(g, ra, qrow, qv, m, l, acc);
       if (!has_b) break;
-      if (t0 + 2 * RT < w1) {
-        R::positions(src, t0 + 3 * RT, w1, tk, pb);
+      if (t0 + 2 * ST < w1) {
+        R::positions(src, t0 + 3 * ST, w1, tk, pb);
         ra.fetch(src, pa, ch, K, V, kb);
       }
       decode_consume<T, D, NQ, NU, EXACT>(g, rb, qrow, qv, m, l, acc);
