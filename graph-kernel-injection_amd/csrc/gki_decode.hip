@@ -282,7 +282,6 @@ __global__ __launch_bounds__(64 * decode_waves<NQ>()) void decode_kernel(
     const typename T::storage* __restrict__ V, typename T::storage* __restrict__ O,
     float* __restrict__ LSE, float* __restrict__ ws, Src src, int kv_rows, int n_tokens,
     int n_splits, int gq) {
-  using S = typename T::storage;
   constexpr int NU = NQ == 1 ? 4 : 3;   // passes per round; two rounds in flight (double-buffered)
   using R = DecodeRound<T, D, NU>;
   constexpr int VEC = R::VEC, LPT = R::LPT, RT = R::RT;
