@@ -502,6 +502,10 @@ def cpu_baseline(cpu_inputs, kept: int, budget_s: float, extra: Optional[dict] =
                                 f"over that time")}
         log(f"[cpu] c4 decode: {n4} (b, h) slice(s) in {t4:.2f} s, {out['c4']['value']:.3f} GB/s")
 
+    out["c5"] = {"value": None, "unit": "TFLOP/s",
+                 "sample": ("not run: the eager path computes all 131072 x 131072 scores of each of "
+                            "a config-5 layer's 16 heads (1.1 TB of fp32 scores; chunked, one head's "
+                            "forward is 4.4 TFLOP, minutes of CPU time at the rates above)")}
     # config 1 runs directly: B1 H4 N1024 D64 fp32 (seed 0), forward + backward
     g1 = torch.Generator().manual_seed(0)
     q1, k1, v1 = (torch.randn(1, 4, 1024, 64, generator=g1).requires_grad_(True) for _ in range(3))
