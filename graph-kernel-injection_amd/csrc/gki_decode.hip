@@ -10,16 +10,18 @@
 //     row can see (per tile its sink run and its window run): S + W positions
 //     per head for n_q = 1;
 //   * decode_kernel: workgroup (bh, split) takes an equal slice of that stream
-//     and each of its 12 waves (8 for several rows) streams a contiguous part of the slice in
-//     rounds of 4 token-row passes (16-byte non-temporal K and V loads, D/8
-//     lanes per row), double-buffered: the next round's loads are issued
+//     and its 12 waves (8 for several rows) take the slice's rounds of 4
+//     token-row passes in turn (wave w: rounds w, w + 12, ..., so the workgroup
+//     sweeps its rows in address order; 16-byte non-temporal K and V loads,
+//     D/8 lanes per row), double-buffered: the next round's loads are issued
 //     before the current one is consumed (scores, wave-local online softmax,
 //     P V), so every CU keeps HBM busy through its compute. No barrier until
 //     the end, where the waves merge in LDS. With one split per head the workgroup writes O and
 //     LSE itself; otherwise it writes (acc[D], m, l) to a workspace and
 //   * combine_kernel (one wave per row) merges the splits:
-//     O = sum acc_s 2^(m_s-M) / sum l_s 2^(m_s-M), LSE = M ln2 + ln L,
-//     with the (O = 0, LSE = 0) sentinel for empty rows.
+//     O = sum acc_s 2^(m_s-M) / sum l_s 2^(m_s-M), LSE = M + log2 L (base 2,
+//     as the forward stores it), with the (O = 0, LSE = 0) sentinel for empty
+//     rows.
 // Cross-workgroup merging goes through a second launch on purpose: publishing
 // partials across XCDs inside one kernel needs agent-scope fences, which on
 // gfx950 write back and invalidate L2.
