@@ -45,6 +45,16 @@ def test_dense_mask_cpu():
         stk.make_dense_mask(65, 128, 16, 32, device="cpu")
 
 
+def test_drop_in_module_names():
+    """The reference module's public names and its backend flag: True here,
+    where the kernel library loads (the op itself needs a GPU)."""
+    for name in ("StreamingMaskSpec", "make_streaming_mask", "make_dense_mask", "streaming_token_mask",
+                 "block_sparse_attention", "reference_block_sparse_attention",
+                 "_BlockSparseFlashAttention"):
+        assert hasattr(stk, name), name
+    assert stk._TRITON_AVAILABLE is True and stk._TRITON_AVAILABLE == _lib.available()
+
+
 def test_spec_and_mask_argument_errors():
     with pytest.raises(ValueError, match="non-negative"):
         stk.StreamingMaskSpec(-1, 4)
