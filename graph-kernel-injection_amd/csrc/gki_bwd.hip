@@ -4,8 +4,8 @@
 // `_BlockSparseFlashAttention.backward` (sparse_triton_kernel.py:719-777):
 //   * `_bwd_preprocess_kernel` (sparse_triton_kernel.py:354-392),
 //       Delta[q] = sum_d fp32(O) * fp32(dO) over the stored O: for 16-bit
-//       inputs inside dq_kernel_16, which runs first and stores Delta * scale
-//       for dK/dV; for fp32 inputs delta_kernel, before the other two.
+//       inputs inside dq_kernel_16, which runs first and stores -Delta for
+//       dK/dV; for fp32 inputs delta_kernel, before the other two.
 //   * dkdv_kernel   <- `_bwd_dkdv_kernel` (sparse_triton_kernel.py:394-509):
 //       one workgroup per 64-row KV tile, loop over the kept q tiles of its
 //       column (CSC list), P = exp(S - LSE) (as exp2 of base-2 terms; the
@@ -271,8 +271,13 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
     floatx4 p[4], ds[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
+      // the dP accumulator starts at -Delta of its four q rows (stored negated
+      // by the dQ kernel), so it ends as dP - Delta and dS / scale = P * acc
+      const int qr0 = rho(t, 4 * grp);
+      const float4 lse4 = *(const float4*)(&slse[buf][qr0]);
+      const float4 ndl4 = *(const float4*)(&sdlt[buf][qr0]);
       floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
-      floatx4 dp = floatx4{0.f, 0.f, 0.f, 0.f};
+      floatx4 dp = floatx4{ndl4.x, ndl4.y, ndl4.z, ndl4.w};
       const int r = rho(t, col);
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
@@ -282,17 +287,17 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
         s = T::mfma(aq, kf[ks], s);
         dp = T::mfma(ad, vf[ks], dp);
       }
-      const int qr0 = rho(t, 4 * grp);
-      const float4 lse4 = *(const float4*)(&slse[buf][qr0]);
-      const float4 dlt4 = *(const float4*)(&sdlt[buf][qr0]);
       const float lv[4] = {lse4.x, lse4.y, lse4.z, lse4.w};          // base-2 LSE
-      const float dv4[4] = {dlt4.x, dlt4.y, dlt4.z, dlt4.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], g.scale_log2, -lv[i]));
         p[t][i] = pv;
-        ds[t][i] = pv * __builtin_fmaf(dp[i], g.scale, -dv4[i]);   // Delta * scale from dQ
+        ds[t][i] = pv * dp[i];   // dS / scale
       }
+    }
+    if (g.ds_scale != 1.f) {   // uniform: the reference's order unless the scale is a power of two
+#pragma unroll
+      for (int t = 0; t < 4; ++t) ds[t] *= g.ds_scale;
     }
     // Masked elements: P = dS = 0 (a bit select, so an exp that overflowed on
     // an invisible element cannot leak). One uniform branch per tile keeps the
@@ -322,6 +327,8 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
   }
 
   // dK/dV accumulators: lane holds rows k_w + 4grp + i, column 16dt + col.
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) dk[dt] *= g.grad_scale;
   if (item.pslot >= 0) {             // a split column: fp32 partials for the reduce
     float* pk = w.partials + ((size_t)bh * w.n_pslots + item.pslot) * 2 * (kTileN * D);
     float* pv = pk + kTileN * D;
@@ -548,9 +555,11 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_16(
       for (int i = 0; i < 8; ++i) part += T::to_float(ho[i]) * T::to_float(hd[i]);
     }
   }
-  // stored and used pre-scaled: dS = P (dP scale - Delta scale), one fma
-  const float dlt = wave_sum16x4(part) * g.scale;
-  if (my_q < g.n_q && grp == 0) Delta[(size_t)bh * g.n_q + my_q] = dlt;
+  // Stored negated: both kernels start their dP accumulators at -Delta, so
+  // they end as dP - Delta and dS / scale = P * acc costs one multiply (the
+  // scale: Geom::ds_scale / grad_scale).
+  const float ndlt = -wave_sum16x4(part);
+  if (my_q < g.n_q && grp == 0) Delta[(size_t)bh * g.n_q + my_q] = ndlt;
 
   floatx4 dq[DT];
 #pragma unroll
@@ -593,7 +602,7 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_16(
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
-      floatx4 dp = floatx4{0.f, 0.f, 0.f, 0.f};
+      floatx4 dp = floatx4{ndlt, ndlt, ndlt, ndlt};
       const int r = rho(t, col);
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
@@ -606,8 +615,12 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_16(
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], g.scale_log2, -lse2));
-        ds[t][i] = pv * __builtin_fmaf(dp[i], g.scale, -dlt);
+        ds[t][i] = pv * dp[i];   // dS / scale
       }
+    }
+    if (g.ds_scale != 1.f) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) ds[t] *= g.ds_scale;
     }
     if (need_mask) {     // masked elements: dS = 0 (bit select, as in the dK/dV kernel)
       const LaneBits vis(row_valid_bits(g, my_q, k0, partial), grp);
@@ -629,8 +642,8 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_16(
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
       uint2 w;
-      w.x = pack2<T>(dq[dt][0], dq[dt][1]);
-      w.y = pack2<T>(dq[dt][2], dq[dt][3]);
+      w.x = pack2<T>(dq[dt][0] * g.grad_scale, dq[dt][1] * g.grad_scale);
+      w.y = pack2<T>(dq[dt][2] * g.grad_scale, dq[dt][3] * g.grad_scale);
       *(uint2*)(dQ + qb + (size_t)my_q * D + 16 * dt + 4 * grp) = w;
     }
   }

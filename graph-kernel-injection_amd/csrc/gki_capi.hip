@@ -69,6 +69,10 @@ void set_scale(Geom& g, float scale) {
   g.q_and = scale == 0.f ? 0u : 0xFFFFFFFFu;
   g.q_xor = scale < 0.f ? 0x80008000u : 0u;
   g.qk_scale_log2 = scale == 0.f ? kLog2e : (scale < 0.f ? -scale : scale) * kLog2e;
+  int e2 = 0;
+  const bool pow2 = scale != 0.f && std::fabs(std::frexp(scale, &e2)) == 0.5f;
+  g.ds_scale = pow2 ? 1.f : scale;
+  g.grad_scale = pow2 ? scale : 1.f;
 }
 
 int make_geom(Geom& g, int dtype, int B, int H, int H_kv, int n_q, int n_kv, int head_dim,

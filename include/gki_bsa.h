@@ -130,7 +130,7 @@ int gki_bsa_fwd(const void* q, const void* k, const void* v, void* o, float* lse
  * [B * H_kv][n_pslots][2][64][head_dim], needed when n_split > 0) and dQ over
  * the CSR list, both over bwd_tile_m x tile_n tiles. `delta` is a caller-owned fp32
  * [B, H, N_Q] workspace for the row terms (its contents on return are internal:
- * Delta for fp32 inputs, Delta * softmax_scale for fp16 / bf16). dq, dk, dv are
+ * Delta for fp32 inputs, -Delta for fp16 / bf16). dq, dk, dv are
  * fully written (no zero-fill needed). */
 int gki_bsa_bwd(const void* q, const void* k, const void* v, const void* o,
                 const void* dout, const float* lse, void* dq, void* dk, void* dv,
