@@ -219,6 +219,12 @@ class _ScheduleCache:
                 self._sched.move_to_end(full)
                 return hit
         value = build()
+        # The build's kernels ran on this thread's current stream; a schedule
+        # becomes visible to every stream and thread once cached, so it is
+        # complete on the device before it is published (builds are rare and
+        # already wait once for their list sizes).
+        if mask.is_cuda:
+            torch.cuda.current_stream(mask.device).synchronize()
         with self._lock:
             self._sched[full] = value
             self._sched.move_to_end(full)
