@@ -175,7 +175,11 @@ __global__ __launch_bounds__(256) void dkdv_reduce_kernel(Geom g, KvWork w,
 // dK / dV, 16-bit. Q and dO tiles row-major in LDS (double-buffered, staged by
 // LDS-DMA); the dV += P^T dO and dK += dS^T Q operands dO / Q come from lds_tr8.
 // ---------------------------------------------------------------------------
-template <typename T, int D>
+// DEFER (Geom::defer_scale): dS is cast as P (dP - Delta) and the scale is
+// applied to the fp32 dK / dQ sums (a power-of-two scale on bf16 inputs, the
+// same products); otherwise dS = P (dP - Delta) scale before the cast, as the
+// reference. A template parameter, so neither form carries a branch.
+template <typename T, int D, bool DEFER>
 __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
     Geom g, const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const uint16_t* __restrict__ V, const uint16_t* __restrict__ dO, uint16_t* __restrict__ dK,
@@ -292,12 +296,8 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
       for (int i = 0; i < 4; ++i) {
         const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], g.scale_log2, -lv[i]));
         p[t][i] = pv;
-        ds[t][i] = pv * dp[i];   // dS / scale
+        ds[t][i] = DEFER ? pv * dp[i] : pv * (dp[i] * g.scale);
       }
-    }
-    if (g.ds_scale != 1.f) {   // uniform: the reference's order unless the scale is a power of two
-#pragma unroll
-      for (int t = 0; t < 4; ++t) ds[t] *= g.ds_scale;
     }
     // Masked elements: P = dS = 0 (a bit select, so an exp that overflowed on
     // an invisible element cannot leak). One uniform branch per tile keeps the
@@ -327,8 +327,10 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
   }
 
   // dK/dV accumulators: lane holds rows k_w + 4grp + i, column 16dt + col.
+  if constexpr (DEFER) {
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt) dk[dt] *= g.grad_scale;
+    for (int dt = 0; dt < DT; ++dt) dk[dt] *= g.scale;
+  }
   if (item.pslot >= 0) {             // a split column: fp32 partials for the reduce
     float* pk = w.partials + ((size_t)bh * w.n_pslots + item.pslot) * 2 * (kTileN * D);
     float* pv = pk + kTileN * D;
@@ -507,7 +509,7 @@ __global__ __launch_bounds__(256, D >= 128 ? 1 : 2) void dkdv_kernel_32(
 // LDS-DMA); the
 // dQ^T += K^T dS^T operand K^T comes from lds_tr8.
 // ---------------------------------------------------------------------------
-template <typename T, int D>
+template <typename T, int D, bool DEFER>
 __global__ __launch_bounds__(256, 2) void dq_kernel_16(
     Geom g, const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const uint16_t* __restrict__ V, const uint16_t* __restrict__ O, const uint16_t* __restrict__ dO,
@@ -556,8 +558,7 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_16(
     }
   }
   // Stored negated: both kernels start their dP accumulators at -Delta, so
-  // they end as dP - Delta and dS / scale = P * acc costs one multiply (the
-  // scale: Geom::ds_scale / grad_scale).
+  // they end as dP - Delta (the scale: see DEFER).
   const float ndlt = -wave_sum16x4(part);
   if (my_q < g.n_q && grp == 0) Delta[(size_t)bh * g.n_q + my_q] = ndlt;
 
@@ -615,12 +616,8 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_16(
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], g.scale_log2, -lse2));
-        ds[t][i] = pv * dp[i];   // dS / scale
+        ds[t][i] = DEFER ? pv * dp[i] : pv * (dp[i] * g.scale);
       }
-    }
-    if (g.ds_scale != 1.f) {
-#pragma unroll
-      for (int t = 0; t < 4; ++t) ds[t] *= g.ds_scale;
     }
     if (need_mask) {     // masked elements: dS = 0 (bit select, as in the dK/dV kernel)
       const LaneBits vis(row_valid_bits(g, my_q, k0, partial), grp);
@@ -642,8 +639,9 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_16(
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
       uint2 w;
-      w.x = pack2<T>(dq[dt][0] * g.grad_scale, dq[dt][1] * g.grad_scale);
-      w.y = pack2<T>(dq[dt][2] * g.grad_scale, dq[dt][3] * g.grad_scale);
+      const float sc = DEFER ? g.scale : 1.f;
+      w.x = pack2<T>(dq[dt][0] * sc, dq[dt][1] * sc);
+      w.y = pack2<T>(dq[dt][2] * sc, dq[dt][3] * sc);
       *(uint2*)(dQ + qb + (size_t)my_q * D + 16 * dt + 4 * grp) = w;
     }
   }
@@ -758,6 +756,34 @@ void launch_delta(const void* o, const void* dout, float* delta, int64_t rows, h
                      (const typename T::storage*)o, (const typename T::storage*)dout, delta, rows);
 }
 
+// dQ first: it also produces Delta, which dK/dV reads
+template <typename T, int D, bool DEFER>
+void launch_bwd16_as(const Geom& g, const void* q, const void* k, const void* v, const void* o,
+                     const void* dout, const float* lse, void* dq, void* dk, void* dv, float* delta,
+                     const int32_t* row_ptr, const int32_t* row_idx, int n_qt, const int32_t* col_ptr,
+                     const int32_t* col_idx, const KvWork& w, hipStream_t stream) {
+  const int BH = g.B * g.H, BHkv = g.B * g.H_kv;
+  hipLaunchKernelGGL((dq_kernel_16<T, D, DEFER>), dim3(n_qt * BH), dim3(256), 0, stream, g,
+                     (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)o,
+                     (const uint16_t*)dout, (uint16_t*)dq, lse, delta, row_ptr, row_idx, n_qt);
+  hipLaunchKernelGGL((dkdv_kernel_16<T, D, DEFER>), dim3(w.n_items * BHkv), dim3(256), 0, stream, g,
+                     (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)dout,
+                     (uint16_t*)dk, (uint16_t*)dv, lse, delta, col_ptr, col_idx, w);
+}
+
+template <typename T, int D>
+void launch_bwd16(const Geom& g, const void* q, const void* k, const void* v, const void* o,
+                  const void* dout, const float* lse, void* dq, void* dk, void* dv, float* delta,
+                  const int32_t* row_ptr, const int32_t* row_idx, int n_qt, const int32_t* col_ptr,
+                  const int32_t* col_idx, const KvWork& w, hipStream_t stream) {
+  if (g.defer_scale)
+    launch_bwd16_as<T, D, true>(g, q, k, v, o, dout, lse, dq, dk, dv, delta, row_ptr, row_idx, n_qt,
+                                col_ptr, col_idx, w, stream);
+  else
+    launch_bwd16_as<T, D, false>(g, q, k, v, o, dout, lse, dq, dk, dv, delta, row_ptr, row_idx, n_qt,
+                                 col_ptr, col_idx, w, stream);
+}
+
 template <int D>
 int launch_bwd(int dtype, const Geom& g, const void* q, const void* k, const void* v, const void* o,
                const void* dout, const float* lse, void* dq, void* dk, void* dv, float* delta,
@@ -778,28 +804,14 @@ int launch_bwd(int dtype, const Geom& g, const void* q, const void* k, const voi
                        (const float*)k, (const float*)v, (const float*)dout, (float*)dq, lse, delta,
                        row_ptr, row_idx, n_qt);
   } else if (dtype == kF16) {
-    // dQ first: it also produces Delta, which dK/dV reads
-    hipLaunchKernelGGL((dq_kernel_16<F16, D>), dim3(n_qt * BH), dim3(256), 0, stream, g,
-                       (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
-                       (const uint16_t*)o, (const uint16_t*)dout, (uint16_t*)dq, lse, delta,
-                       row_ptr, row_idx, n_qt);
-    hipLaunchKernelGGL((dkdv_kernel_16<F16, D>), kv_grid, dim3(256), 0, stream, g,
-                       (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
-                       (const uint16_t*)dout, (uint16_t*)dk, (uint16_t*)dv, lse, delta, col_ptr,
-                       col_idx, w);
+    launch_bwd16<F16, D>(g, q, k, v, o, dout, lse, dq, dk, dv, delta, row_ptr, row_idx, n_qt,
+                         col_ptr, col_idx, w, stream);
     if (w.n_split > 0)
       hipLaunchKernelGGL((dkdv_reduce_kernel<F16, D>), red_grid, dim3(256), 0, stream, g, w,
                          (uint16_t*)dk, (uint16_t*)dv);
   } else {
-    // dQ first: it also produces Delta, which dK/dV reads
-    hipLaunchKernelGGL((dq_kernel_16<BF16, D>), dim3(n_qt * BH), dim3(256), 0, stream, g,
-                       (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
-                       (const uint16_t*)o, (const uint16_t*)dout, (uint16_t*)dq, lse, delta,
-                       row_ptr, row_idx, n_qt);
-    hipLaunchKernelGGL((dkdv_kernel_16<BF16, D>), kv_grid, dim3(256), 0, stream, g,
-                       (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
-                       (const uint16_t*)dout, (uint16_t*)dk, (uint16_t*)dv, lse, delta, col_ptr,
-                       col_idx, w);
+    launch_bwd16<BF16, D>(g, q, k, v, o, dout, lse, dq, dk, dv, delta, row_ptr, row_idx, n_qt,
+                         col_ptr, col_idx, w, stream);
     if (w.n_split > 0)
       hipLaunchKernelGGL((dkdv_reduce_kernel<BF16, D>), red_grid, dim3(256), 0, stream, g, w,
                          (uint16_t*)dk, (uint16_t*)dv);

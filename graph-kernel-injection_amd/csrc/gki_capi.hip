@@ -69,10 +69,7 @@ void set_scale(Geom& g, float scale) {
   g.q_and = scale == 0.f ? 0u : 0xFFFFFFFFu;
   g.q_xor = scale < 0.f ? 0x80008000u : 0u;
   g.qk_scale_log2 = scale == 0.f ? kLog2e : (scale < 0.f ? -scale : scale) * kLog2e;
-  int e2 = 0;
-  const bool pow2 = scale != 0.f && std::fabs(std::frexp(scale, &e2)) == 0.5f;
-  g.ds_scale = pow2 ? 1.f : scale;
-  g.grad_scale = pow2 ? scale : 1.f;
+  g.defer_scale = 0;   // reference order; make_geom sets it where exact
 }
 
 int make_geom(Geom& g, int dtype, int B, int H, int H_kv, int n_q, int n_kv, int head_dim,
@@ -103,6 +100,13 @@ int make_geom(Geom& g, int dtype, int B, int H, int H_kv, int n_q, int n_kv, int
   g.n_kv = n_kv;
   g.q_off = n_kv - n_q;
   set_scale(g, scale);
+  // 16-bit backward: cast P (dP - Delta) and scale the fp32 dQ / dK sums when
+  // that gives the same products, i.e. a power-of-two scale on bf16 inputs
+  // (fp32's exponent range, so the unscaled value neither overflows nor
+  // underflows differently); fp16 keeps the reference order, whose cast of the
+  // scaled dS has 1/scale more headroom below the fp16 maximum.
+  int e2 = 0;
+  g.defer_scale = dtype == kBF16 && scale != 0.f && std::fabs(std::frexp(scale, &e2)) == 0.5f;
   g.causal = causal ? 1 : 0;
   g.sink = sink;
   g.window = window;

@@ -355,11 +355,11 @@ struct Geom {
   float qk_scale_log2;
   uint32_t q_and, q_xor;
   // 16-bit backward: dS = P (dP - Delta) scale is cast to 16 bits before the
-  // dK / dQ products. For a power-of-two scale (1/8 at head_dim 64) the cast
-  // commutes with the scale, so the kernels cast P (dP - Delta) and scale the
-  // fp32 sums once (ds_scale = 1, grad_scale = scale); for any other scale they
-  // keep the reference order (ds_scale = scale, grad_scale = 1).
-  float ds_scale, grad_scale;
+  // dK / dQ products. For a power-of-two scale (1/8 at head_dim 64) on bf16
+  // inputs the cast commutes with the scale, so the kernels may cast
+  // P (dP - Delta) and scale the fp32 sums once instead (defer_scale = 1);
+  // otherwise they keep the reference order (defer_scale = 0).
+  int defer_scale;
   int causal, sink, window;
   // original block mask (used only for tiles flagged partial)
   const int32_t* mask;
