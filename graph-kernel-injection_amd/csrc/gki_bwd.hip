@@ -276,7 +276,7 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       // the dP accumulator starts at -Delta of its four q rows (stored negated
-      // by the dQ kernel), so it ends as dP - Delta and dS / scale = P * acc
+      // by the dQ kernel), so it ends as dP - Delta: dS = P * acc * scale
       const int qr0 = rho(t, 4 * grp);
       const float4 lse4 = *(const float4*)(&slse[buf][qr0]);
       const float4 ndl4 = *(const float4*)(&sdlt[buf][qr0]);
