@@ -23,6 +23,9 @@ CSRC = PKG_ROOT / "csrc"
 REPO_ROOT = PKG_ROOT.parent
 BUILD_DIR = REPO_ROOT / "_build" / "gki"
 LIB_PATH = PKG_ROOT / "gki" / "libgki_bsa.so"
+# a C++ caller of the C ABI alone (hipMalloc, no torch), run by a GPU test
+EXAMPLE_SRC = REPO_ROOT / "tests" / "capi" / "capi_forward_example.cpp"
+EXAMPLE_EXE = REPO_ROOT / "tests" / "capi" / "capi_forward_example"
 
 ARCH = "gfx950"
 HIPCC_FLAGS = [
@@ -72,7 +75,22 @@ def build(verbose: bool = True) -> Path:
     os.replace(tmp, LIB_PATH)
     if verbose:
         print(f"[gki] built {LIB_PATH} from {len(sources)} HIP sources for {ARCH}")
+    if EXAMPLE_SRC.exists():
+        _build_example(hipcc)
+        if verbose:
+            print(f"[gki] built {EXAMPLE_EXE} against {LIB_PATH.name}")
     return LIB_PATH
+
+
+def _build_example(hipcc: str) -> None:
+    """Link the C-ABI example against the in-tree library (found via its rpath)."""
+    rpath = os.path.relpath(LIB_PATH.parent, EXAMPLE_EXE.parent)
+    cmd = [hipcc, *HIPCC_FLAGS, str(EXAMPLE_SRC), "-o", str(EXAMPLE_EXE),
+           f"-L{LIB_PATH.parent}", "-lgki_bsa", f"-Wl,-rpath,$ORIGIN/{rpath}"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        err = "\n".join(l for l in res.stderr.splitlines() if "packed-fp32-ops" not in l)
+        raise RuntimeError(f"hipcc failed on {EXAMPLE_SRC.name}:\n{err}")
 
 
 if __name__ == "__main__":
