@@ -7,6 +7,7 @@
 #include <algorithm>
 #include <cmath>
 #include <mutex>
+#include <vector>
 
 #include "gki_bsa.h"
 #include "gki_common.cuh"
@@ -33,7 +34,7 @@ int check_launch(const char* what) {
 int fwd_tile_m(int dtype);
 int fwd_dispatch(int dtype, int head_dim, const Geom& g, const void* q, const void* k, const void* v,
                  void* o, float* lse, const int32_t* row_ptr, const int32_t* row_idx, int n_qt,
-                 hipStream_t stream);
+                 const int32_t* wg_order, hipStream_t stream);
 int bwd_dispatch(int dtype, int head_dim, const Geom& g, const void* q, const void* k, const void* v,
                  const void* o, const void* dout, const float* lse, void* dq, void* dk, void* dv,
                  float* delta, const int32_t* row_ptr, const int32_t* row_idx, int n_qt,
@@ -204,7 +205,7 @@ using namespace gki;
 
 extern "C" {
 
-int gki_abi_version(void) { return 4; }
+int gki_abi_version(void) { return 5; }
 
 const char* gki_last_error(void) { return g_last_error.c_str(); }
 
@@ -221,9 +222,10 @@ int gki_tile_sizes(int32_t* fwd_tile_m_16, int32_t* fwd_tile_m_32, int32_t* bwd_
 
 int gki_bsa_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int32_t dtype,
                 int32_t B, int32_t H, int32_t H_kv, int32_t n_q, int32_t n_kv, int32_t head_dim,
-                const int32_t* row_ptr, const int32_t* row_idx, int32_t n_qt, const int32_t* mask,
-                int32_t n_qb, int32_t n_kb, int32_t block_m, int32_t block_n, float softmax_scale,
-                int32_t is_causal, int32_t sink_size, int32_t window_size, void* stream) {
+                const int32_t* row_ptr, const int32_t* row_idx, int32_t n_qt, const int32_t* wg_order,
+                const int32_t* mask, int32_t n_qb, int32_t n_kb, int32_t block_m, int32_t block_n,
+                float softmax_scale, int32_t is_causal, int32_t sink_size, int32_t window_size,
+                void* stream) {
   Geom g;
   if (int rc = make_geom(g, dtype, B, H, H_kv, n_q, n_kv, head_dim, mask, n_qb, n_kb, block_m, block_n,
                          softmax_scale, is_causal, sink_size, window_size))
@@ -232,7 +234,32 @@ int gki_bsa_fwd(const void* q, const void* k, const void* v, void* o, float* lse
   GKI_REQUIRE(all_aligned16(q, k, v, o), 1, "gki_bsa_fwd: q, k, v, o must be 16-byte aligned");
   const int tm = fwd_tile_m(dtype);
   GKI_REQUIRE(n_qt == (n_q + tm - 1) / tm, 1, "gki_bsa_fwd: schedule row count mismatch");
-  return fwd_dispatch(dtype, head_dim, g, q, k, v, o, lse, row_ptr, row_idx, n_qt, (hipStream_t)stream);
+  GKI_REQUIRE((int64_t)n_qt * B * H < (1ll << 31), 1, "gki_bsa_fwd: grid too large");
+  return fwd_dispatch(dtype, head_dim, g, q, k, v, o, lse, row_ptr, row_idx, n_qt, wg_order,
+                      (hipStream_t)stream);
+}
+
+int gki_fwd_order(const int32_t* row_ptr, int32_t n_qt, int32_t bh, int32_t* order) {
+  GKI_REQUIRE(row_ptr && order, 1, "gki_fwd_order: null pointer");
+  GKI_REQUIRE(n_qt >= 1 && bh >= 1 && (int64_t)n_qt * bh < (1ll << 31), 1,
+              "gki_fwd_order: n_qt and bh must be positive, n_qt * bh < 2^31");
+  std::vector<int32_t> len(n_qt);
+  for (int qt = 0; qt < n_qt; ++qt) {
+    len[qt] = row_ptr[qt + 1] - row_ptr[qt];
+    GKI_REQUIRE(len[qt] >= 0, 1, "gki_fwd_order: row_ptr must be non-decreasing");
+  }
+  // the launch's logical ids are (b * H + h) * n_qt + qt, split into one
+  // contiguous range per XCD; each range is reordered on its own (its q tiles
+  // stay on that XCD, so neighbouring tiles of a head still share its L2),
+  // longest kept-tile list first, ties in logical order
+  const int n = n_qt * bh;
+  for (int x = 0; x < kXcd; ++x) {
+    const int lo = xcd_start(x, n), hi = x + 1 < kXcd ? xcd_start(x + 1, n) : n;
+    for (int l = lo; l < hi; ++l) order[l] = l;
+    std::stable_sort(order + lo, order + hi,
+                     [&](int32_t a, int32_t b) { return len[a % n_qt] > len[b % n_qt]; });
+  }
+  return 0;
 }
 
 int gki_bsa_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout,

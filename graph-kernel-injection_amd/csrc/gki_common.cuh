@@ -509,11 +509,25 @@ __device__ inline bool tile_all_visible(const Geom& g, int q_lo, int q_hi, int k
 // XCD-aware remap: hardware dispatches workgroup b to XCD b % 8. Give each XCD
 // one contiguous range of logical ids so neighbouring q tiles of one head (which
 // share most K/V tiles) run on the same XCD and hit in its L2.
-__device__ inline int xcd_remap(int b, int n) {
-  constexpr int kXcd = 8;
-  const int xcd = b % kXcd, local = b / kXcd;
+constexpr int kXcd = 8;
+// First logical id of XCD x's range (of n); the range holds n / 8 ids, one more
+// for the first n % 8 XCDs (as many as the hardware hands that XCD).
+__host__ __device__ inline int xcd_start(int x, int n) {
   const int per = n / kXcd, rem = n % kXcd;
-  return (xcd < rem) ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+  return x < rem ? x * (per + 1) : rem * (per + 1) + (x - rem) * per;
+}
+__host__ __device__ inline int xcd_remap(int b, int n) { return xcd_start(b % kXcd, n) + b / kXcd; }
+
+// Work unit of workgroup b in a launch over n units: its XCD-remapped logical
+// id, or, with an order table (gki_fwd_order), the unit that table lists at
+// that id (each XCD's range sorted heaviest first, so the units dispatched last
+// are the short ones and the launch ends with less idle tail). -1 (the
+// workgroup exits) for a table entry outside 0 .. n-1.
+__device__ inline int work_of(int b, int n, const int32_t* order) {
+  const int l = xcd_remap(b, n);
+  if (order == nullptr) return l;
+  const int w = __builtin_amdgcn_readfirstlane(order[l]);
+  return (unsigned)w < (unsigned)n ? w : -1;
 }
 
 // Reductions across the 4 lane groups (lanes l, l^16, l^32, l^48) with the

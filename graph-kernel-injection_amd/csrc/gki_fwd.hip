@@ -58,7 +58,8 @@ template <typename T, int D>
 __global__ __launch_bounds__(kFwdThreads, D <= 64 ? 4 : 2) void fwd_kernel_16(
     Geom g, const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const uint16_t* __restrict__ V, uint16_t* __restrict__ O, float* __restrict__ LSE,
-    const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ row_idx, int n_qt) {
+    const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ row_idx, int n_qt,
+    const int32_t* __restrict__ wg_order) {
   constexpr int KS = (D + 31) / 32;   // k-steps of the QK^T contraction
   constexpr int DT = D / 16;          // 16-row tiles of O^T
   constexpr int RB = kFwdRB;
@@ -68,7 +69,8 @@ __global__ __launch_bounds__(kFwdThreads, D <= 64 ? 4 : 2) void fwd_kernel_16(
   __shared__ __align__(16) uint16_t sv[2][kTileN * D];
 
   const int n_wg = n_qt * g.B * g.H;
-  const int wg = xcd_remap(blockIdx.x, n_wg);
+  const int wg = work_of(blockIdx.x, n_wg, wg_order);
+  if (wg < 0) return;
   const int bh = wg / n_qt, qt = wg - bh * n_qt;
   const size_t qb = (size_t)bh * g.n_q * D;
   const size_t kb = (size_t)kv_bh(g, bh) * g.n_kv * D;
@@ -246,7 +248,7 @@ template <int D>
 __global__ __launch_bounds__(256, 2) void fwd_kernel_32(
     Geom g, const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     float* __restrict__ O, float* __restrict__ LSE, const int32_t* __restrict__ row_ptr,
-    const int32_t* __restrict__ row_idx, int n_qt) {
+    const int32_t* __restrict__ row_idx, int n_qt, const int32_t* __restrict__ wg_order) {
   constexpr int KS = D / 4;
   constexpr int DT = D / 16;
   constexpr int CPR = D / 4;           // 16-byte chunks per row
@@ -256,7 +258,8 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel_32(
   __shared__ __align__(16) Smem sm;
 
   const int n_wg = n_qt * g.B * g.H;
-  const int wg = xcd_remap(blockIdx.x, n_wg);
+  const int wg = work_of(blockIdx.x, n_wg, wg_order);
+  if (wg < 0) return;
   const int bh = wg / n_qt, qt = wg - bh * n_qt;
   const size_t qb = (size_t)bh * g.n_q * D;
   const size_t kb = (size_t)kv_bh(g, bh) * g.n_kv * D;
@@ -378,19 +381,20 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel_32(
 template <int D>
 int launch_fwd(int dtype, const Geom& g, const void* q, const void* k, const void* v, void* o,
                float* lse, const int32_t* row_ptr, const int32_t* row_idx, int n_qt,
-               hipStream_t stream) {
+               const int32_t* wg_order, hipStream_t stream) {
   const int grid = n_qt * g.B * g.H;
   if (dtype == kF32) {
     hipLaunchKernelGGL(fwd_kernel_32<D>, dim3(grid), dim3(256), 0, stream, g, (const float*)q,
-                       (const float*)k, (const float*)v, (float*)o, lse, row_ptr, row_idx, n_qt);
+                       (const float*)k, (const float*)v, (float*)o, lse, row_ptr, row_idx, n_qt,
+                       wg_order);
   } else if (dtype == kF16) {
     hipLaunchKernelGGL((fwd_kernel_16<F16, D>), dim3(grid), dim3(kFwdThreads), 0, stream, g,
                        (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, lse,
-                       row_ptr, row_idx, n_qt);
+                       row_ptr, row_idx, n_qt, wg_order);
   } else {
     hipLaunchKernelGGL((fwd_kernel_16<BF16, D>), dim3(grid), dim3(kFwdThreads), 0, stream, g,
                        (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, lse,
-                       row_ptr, row_idx, n_qt);
+                       row_ptr, row_idx, n_qt, wg_order);
   }
   return check_launch("gki_bsa_fwd");
 }
@@ -401,12 +405,12 @@ int fwd_tile_m(int dtype) { return dtype == kF32 ? kTileM : kTileMF; }
 
 int fwd_dispatch(int dtype, int head_dim, const Geom& g, const void* q, const void* k, const void* v,
                  void* o, float* lse, const int32_t* row_ptr, const int32_t* row_idx, int n_qt,
-                 hipStream_t stream) {
+                 const int32_t* wg_order, hipStream_t stream) {
   switch (head_dim) {
-    case 16: return launch_fwd<16>(dtype, g, q, k, v, o, lse, row_ptr, row_idx, n_qt, stream);
-    case 32: return launch_fwd<32>(dtype, g, q, k, v, o, lse, row_ptr, row_idx, n_qt, stream);
-    case 64: return launch_fwd<64>(dtype, g, q, k, v, o, lse, row_ptr, row_idx, n_qt, stream);
-    case 128: return launch_fwd<128>(dtype, g, q, k, v, o, lse, row_ptr, row_idx, n_qt, stream);
+    case 16: return launch_fwd<16>(dtype, g, q, k, v, o, lse, row_ptr, row_idx, n_qt, wg_order, stream);
+    case 32: return launch_fwd<32>(dtype, g, q, k, v, o, lse, row_ptr, row_idx, n_qt, wg_order, stream);
+    case 64: return launch_fwd<64>(dtype, g, q, k, v, o, lse, row_ptr, row_idx, n_qt, wg_order, stream);
+    case 128: return launch_fwd<128>(dtype, g, q, k, v, o, lse, row_ptr, row_idx, n_qt, wg_order, stream);
     default: return fail(2, "unsupported head_dim " + std::to_string(head_dim));
   }
 }

@@ -33,7 +33,8 @@ SIGNATURES = {
                                            _c_ptr]),
     "gki_dkdv_items": (ctypes.c_int, [_c_ptr, _c_int, _c_int, _c_int, _c_int, _c_ptr, _c_ptr, _c_ptr,
                                       _c_ptr, _c_ptr]),
-    "gki_bsa_fwd": (ctypes.c_int, [_c_ptr] * 5 + [_c_int] * 7 + [_c_ptr, _c_ptr, _c_int, _c_ptr]
+    "gki_fwd_order": (ctypes.c_int, [_c_ptr, _c_int, _c_int, _c_ptr]),
+    "gki_bsa_fwd": (ctypes.c_int, [_c_ptr] * 5 + [_c_int] * 7 + [_c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr]
                     + [_c_int] * 4 + [_c_float] + [_c_int] * 3 + [_c_ptr]),
     "gki_bsa_bwd": (ctypes.c_int, [_c_ptr] * 10 + [_c_int] * 7
                     + [_c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_int]      # CSR, CSC, n_kt

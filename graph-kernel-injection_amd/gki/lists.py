@@ -60,6 +60,7 @@ class BlockLists:
 class FwdSchedule:
     lists: BlockLists         # CSR used; over fwd tiles (n_qt x n_kt)
     n_qt: int
+    key: tuple = ()           # its schedule-cache key (the order tables extend it)
 
 
 @dataclass(frozen=True)
@@ -253,13 +254,31 @@ def fwd_schedule(mask: torch.Tensor, n_q: int, n_kv: int, block_m: int, block_n:
     tm = ts["fwd_tile_m_32"] if fp32 else ts["fwd_tile_m_16"]
     tn = ts["tile_n"]
 
+    key = ("fwd", n_q, n_kv, block_m, block_n, tm, tn, bool(is_causal), sink, window)
+
     def build() -> FwdSchedule:
         tiles = tile_matrix(mask, n_q, n_kv, block_m, block_n, tm, tn, is_causal, sink, window)
         lists = _lists_of(tiles, need_cols=False)
-        return FwdSchedule(lists, lists.n_rows)
+        return FwdSchedule(lists, lists.n_rows, key)
 
-    key = ("fwd", n_q, n_kv, block_m, block_n, tm, tn, bool(is_causal), sink, window)
     return _CACHE.get(mask, key, build)
+
+
+def fwd_order(mask: torch.Tensor, sched: FwdSchedule, bh: int) -> torch.Tensor:
+    """Workgroup order of the forward launch over ``bh`` = B * H heads
+    (``gki_fwd_order``: each XCD's share of (b, h, q tile) units, longest
+    kept-tile list first), a device int32 tensor [n_qt * bh], cached with the
+    schedule."""
+
+    def build() -> torch.Tensor:
+        lib = _lib.load()
+        row_ptr = sched.lists.row_ptr.to("cpu").contiguous()
+        order = torch.empty(sched.n_qt * bh, dtype=torch.int32)
+        _lib.check(lib.gki_fwd_order(row_ptr.data_ptr(), sched.n_qt, bh, order.data_ptr()),
+                   "gki_fwd_order")
+        return order.to(mask.device)
+
+    return _CACHE.get(mask, sched.key + ("order", bh), build)
 
 
 def dkdv_items(col_ptr_host: torch.Tensor, group: int, bh_kv: int, max_chunk: int = 0):

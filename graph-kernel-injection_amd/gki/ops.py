@@ -24,7 +24,7 @@ from typing import Optional, Tuple
 import torch
 
 from . import _lib
-from .lists import _CACHE, bwd_schedule, decode_schedule, fwd_schedule
+from .lists import _CACHE, bwd_schedule, decode_schedule, fwd_order, fwd_schedule
 
 _DTYPE_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 _HEAD_DIMS = (16, 32, 64, 128)
@@ -197,10 +197,12 @@ def _attention_forward(q, k, v, block_mask, softmax_scale, block_m, block_n, is_
             lse = torch.empty((B, H, N_Q), dtype=torch.float32, device=dev)
             sched = fwd_schedule(block_mask, N_Q, N_KV, block_m, block_n, bool(is_causal),
                                  int(sink_size), int(window_size), q.dtype == torch.float32)
+            order = fwd_order(block_mask, sched, B * H)
             _lib.check(lib.gki_bsa_fwd(
                 q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), dtype,
                 B, H, H_kv, N_Q, N_KV, D, sched.lists.row_ptr.data_ptr(),
-                sched.lists.row_buf.data_ptr(), sched.n_qt, *common, stream), "gki_bsa_fwd")
+                sched.lists.row_buf.data_ptr(), sched.n_qt, order.data_ptr(), *common, stream),
+                "gki_bsa_fwd")
 
     return o, lse, q, k, v, block_mask, q_offset
 

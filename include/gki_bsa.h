@@ -42,8 +42,9 @@
 extern "C" {
 #endif
 
-/* ABI version (currently 4: grouped-query attention, H_kv after H; dK/dV work
- * items from gki_dkdv_items, whose chunk can be capped by max_chunk). */
+/* ABI version (currently 5: grouped-query attention, H_kv after H; dK/dV work
+ * items from gki_dkdv_items, whose chunk can be capped by max_chunk; the
+ * forward's optional workgroup order from gki_fwd_order). */
 int gki_abi_version(void);
 
 /* Message of the last failing call on this thread. */
@@ -111,17 +112,29 @@ int gki_dkdv_items(const int32_t* col_ptr, int32_t n_kt, int32_t group, int32_t 
                    int32_t max_chunk, int32_t* items, int32_t* n_items, int32_t* split,
                    int32_t* n_split, int32_t* n_pslots);
 
+/* Order of the forward grid's workgroups (host arrays; no reference
+ * counterpart -- the reference's grid runs its programs in index order,
+ * sparse_triton_kernel.py:662-682). row_ptr: the forward CSR row pointers
+ * (n_qt + 1, host copy); bh: B * H. Writes order[n_qt * bh], a permutation of
+ * the work units (b * H + h) * n_qt + qt: the units each XCD receives (one
+ * contiguous range per XCD, as the kernels map workgroups) sorted by
+ * descending kept-tile count, ties in index order, so that each XCD ends its
+ * share with the short units. Results do not depend on the order. */
+int gki_fwd_order(const int32_t* row_ptr, int32_t n_qt, int32_t bh, int32_t* order);
+
 /* Prefill forward: replaces the `_fwd_kernel` launch in
  * `_BlockSparseFlashAttention.forward` (sparse_triton_kernel.py:662-682).
  * O = softmax(mask(Q K^T * scale)) V, LSE (base 2) = m + log2(l), 0 for empty rows.
  * row_ptr/row_idx: CSR over ceil(n_q/fwd_tile_m) q tiles (fwd_tile_m_16 or
- * fwd_tile_m_32 by dtype) of kept kv tiles. */
+ * fwd_tile_m_32 by dtype) of kept kv tiles. wg_order: NULL (index order) or a
+ * device copy of gki_fwd_order's table for this CSR and B * H (a workgroup
+ * whose entry is out of range does nothing). */
 int gki_bsa_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
                 int32_t dtype, int32_t B, int32_t H, int32_t H_kv, int32_t n_q, int32_t n_kv,
                 int32_t head_dim, const int32_t* row_ptr, const int32_t* row_idx,
-                int32_t n_qt, const int32_t* mask, int32_t n_qb, int32_t n_kb,
-                int32_t block_m, int32_t block_n, float softmax_scale, int32_t is_causal,
-                int32_t sink_size, int32_t window_size, void* stream);
+                int32_t n_qt, const int32_t* wg_order, const int32_t* mask, int32_t n_qb,
+                int32_t n_kb, int32_t block_m, int32_t block_n, float softmax_scale,
+                int32_t is_causal, int32_t sink_size, int32_t window_size, void* stream);
 
 /* Backward: replaces the three launches in `_BlockSparseFlashAttention.backward`
  * (sparse_triton_kernel.py:719-777): the row terms Delta = rowsum(O * dO), dK/dV

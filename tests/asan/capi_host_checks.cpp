@@ -6,6 +6,8 @@
 //    checked against the work-list invariants;
 //  * gki_rolling_stream against a brute-force count of the positions the last
 //    n_q queries of a StreamingLLM cache can see;
+//  * gki_fwd_order on random row lists into an exactly sized table: a
+//    permutation that keeps each XCD's contiguous share, heaviest first;
 //  * every launching entry point rejecting bad arguments with an error code
 //    and a message, before it touches the device.
 #include <algorithm>
@@ -134,23 +136,23 @@ static void check_rejections() {
     CHECK(rc != 0 && !msg.empty(), "%s: rc %d, message '%s'", what, rc, msg.c_str());
   };
   // forward: bad dtype, bad head_dim, null tensors, misaligned pointers, wrong list size
-  rejected(gki_bsa_fwd(p, p, p, p, f, 7, 1, 1, 1, 64, 64, 64, ip, ip, 1, ip, 1, 1, 64, 64, 0.125f, 1, 4,
+  rejected(gki_bsa_fwd(p, p, p, p, f, 7, 1, 1, 1, 64, 64, 64, ip, ip, 1, nullptr, ip, 1, 1, 64, 64, 0.125f, 1, 4,
                        16, nullptr), "fwd dtype 7");
-  rejected(gki_bsa_fwd(p, p, p, p, f, 2, 1, 1, 1, 64, 64, 48, ip, ip, 1, ip, 1, 1, 64, 64, 0.125f, 1, 4,
+  rejected(gki_bsa_fwd(p, p, p, p, f, 2, 1, 1, 1, 64, 64, 48, ip, ip, 1, nullptr, ip, 1, 1, 64, 64, 0.125f, 1, 4,
                        16, nullptr), "fwd head_dim 48");
-  rejected(gki_bsa_fwd(nullptr, p, p, p, f, 2, 1, 1, 1, 64, 64, 64, ip, ip, 1, ip, 1, 1, 64, 64, 0.125f,
+  rejected(gki_bsa_fwd(nullptr, p, p, p, f, 2, 1, 1, 1, 64, 64, 64, ip, ip, 1, nullptr, ip, 1, 1, 64, 64, 0.125f,
                        1, 4, 16, nullptr), "fwd null q");
-  rejected(gki_bsa_fwd(buf + 2, p, p, p, f, 2, 1, 1, 1, 64, 64, 64, ip, ip, 1, ip, 1, 1, 64, 64, 0.125f,
+  rejected(gki_bsa_fwd(buf + 2, p, p, p, f, 2, 1, 1, 1, 64, 64, 64, ip, ip, 1, nullptr, ip, 1, 1, 64, 64, 0.125f,
                        1, 4, 16, nullptr), "fwd misaligned q");
-  rejected(gki_bsa_fwd(p, p, p, p, f, 2, 1, 1, 1, 64, 64, 64, ip, ip, 3, ip, 1, 1, 64, 64, 0.125f, 1, 4,
+  rejected(gki_bsa_fwd(p, p, p, p, f, 2, 1, 1, 1, 64, 64, 64, ip, ip, 3, nullptr, ip, 1, 1, 64, 64, 0.125f, 1, 4,
                        16, nullptr), "fwd schedule rows");
-  rejected(gki_bsa_fwd(p, p, p, p, f, 2, 1, 4, 3, 64, 64, 64, ip, ip, 1, ip, 1, 1, 64, 64, 0.125f, 1, 4,
+  rejected(gki_bsa_fwd(p, p, p, p, f, 2, 1, 4, 3, 64, 64, 64, ip, ip, 1, nullptr, ip, 1, 1, 64, 64, 0.125f, 1, 4,
                        16, nullptr), "fwd H_kv not dividing H");
-  rejected(gki_bsa_fwd(p, p, p, p, f, 2, 1, 1, 1, 64, 64, 64, ip, ip, 1, ip, 2, 1, 64, 64, 0.125f, 1, 4,
+  rejected(gki_bsa_fwd(p, p, p, p, f, 2, 1, 1, 1, 64, 64, 64, ip, ip, 1, nullptr, ip, 2, 1, 64, 64, 0.125f, 1, 4,
                        16, nullptr), "fwd mask shape");
-  rejected(gki_bsa_fwd(p, p, p, p, f, 2, 1, 1, 1, 64, 64, 64, ip, ip, 1, ip, 1, 1, 64, 64,
+  rejected(gki_bsa_fwd(p, p, p, p, f, 2, 1, 1, 1, 64, 64, 64, ip, ip, 1, nullptr, ip, 1, 1, 64, 64,
                        __builtin_inff(), 1, 4, 16, nullptr), "fwd infinite scale");
-  rejected(gki_bsa_fwd(p, p, p, p, f, 2, 1, 1, 1, 64, 64, 64, ip, ip, 1, ip, 1, 1, 64, 64, 0.125f, 1, -1,
+  rejected(gki_bsa_fwd(p, p, p, p, f, 2, 1, 1, 1, 64, 64, 64, ip, ip, 1, nullptr, ip, 1, 1, 64, 64, 0.125f, 1, -1,
                        16, nullptr), "fwd negative sink");
   // backward: inconsistent work list, missing partials, schedule shape
   rejected(gki_bsa_bwd(p, p, p, p, p, f, p, p, p, f, 2, 1, 1, 1, 64, 64, 64, ip, ip, 1, ip, ip, 1, ip, 0,
@@ -183,11 +185,49 @@ static void check_rejections() {
   CHECK(gki_tile_sizes(t, t + 1, t + 2, t + 3, t + 4, t + 5) == 0 && t[3] == 64, "tile sizes");
   CHECK(gki_tile_sizes(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr) == 0, "tile sizes, nulls");
   CHECK(gki_bsa_decode_workspace_floats(8, 32, 1, 128, 4) == 8ll * 32 * 4 * 130, "workspace floats");
+  const int32_t down[3] = {0, 4, 2};
+  int32_t ord[4];
+  rejected(gki_fwd_order(down, 2, 2, ord), "order of a decreasing row_ptr");
+  rejected(gki_fwd_order(nullptr, 2, 2, ord), "order, null row_ptr");
+  rejected(gki_fwd_order(down, 0, 2, ord), "order, no q tiles");
+  rejected(gki_fwd_order(down, 1 << 20, 1 << 12, ord), "order, table too large");
+}
+
+static void check_fwd_order(std::mt19937& rng) {
+  for (int trial = 0; trial < 500; ++trial) {
+    const int n_qt = 1 + (int)(rng() % 200);
+    const int bh = 1 + (int)(rng() % 40);
+    std::vector<int32_t> row_ptr(n_qt + 1, 0);
+    for (int qt = 0; qt < n_qt; ++qt) row_ptr[qt + 1] = row_ptr[qt] + (int32_t)(rng() % 6);
+    const int n = n_qt * bh;
+    std::vector<int32_t> order(n, -1);
+    const int rc = gki_fwd_order(row_ptr.data(), n_qt, bh, order.data());
+    CHECK(rc == 0, "gki_fwd_order rc %d (%s)", rc, gki_last_error());
+    if (rc) continue;
+    // XCD x's share: the n / 8 (+1 for x < n % 8) logical ids after XCD x-1's
+    int lo = 0;
+    for (int x = 0; x < 8; ++x) {
+      const int hi = lo + n / 8 + (x < n % 8 ? 1 : 0);
+      std::vector<int32_t> share(order.begin() + lo, order.begin() + hi);
+      for (int i = lo; i < hi; ++i) {
+        CHECK(order[i] >= lo && order[i] < hi, "unit %d left XCD %d's share", order[i], x);
+        if (i > lo) {
+          const int la = row_ptr[order[i - 1] % n_qt + 1] - row_ptr[order[i - 1] % n_qt];
+          const int lb = row_ptr[order[i] % n_qt + 1] - row_ptr[order[i] % n_qt];
+          CHECK(la > lb || (la == lb && order[i - 1] < order[i]), "share of XCD %d out of order", x);
+        }
+      }
+      std::sort(share.begin(), share.end());
+      CHECK(std::unique(share.begin(), share.end()) == share.end(), "repeated unit in XCD %d", x);
+      lo = hi;
+    }
+  }
 }
 
 int main() {
   std::mt19937 rng(1234);
   check_work_lists(rng);
+  check_fwd_order(rng);
   check_rolling_stream(rng);
   check_rejections();
   if (g_fail) {

@@ -1,9 +1,11 @@
 // The C-ABI forward from a C++ caller with no Python and no torch: device
 // buffers from hipMalloc, the StreamingLLM block mask, the forward kernel's
-// tile classes and CSR list built by the library on the GPU, then
-// gki_bsa_fwd (the sequence a C / cgo / JNI binding follows). The output and
-// LSE are compared with a double-precision attention over the token rule
-// computed here on the host; a schedule of the wrong size must be rejected.
+// tile classes and CSR list built by the library on the GPU, the workgroup
+// order from a host copy of the row pointers, then gki_bsa_fwd (the sequence a
+// C / cgo / JNI binding follows). The output and LSE are compared with a
+// double-precision attention over the token rule computed here on the host and
+// with an index-order launch (same bits); a schedule of the wrong size must be
+// rejected.
 // Built by graph-kernel-injection_amd/build.py, run by
 // tests/test_gpu_capi_example.py on an MI355X.
 #include <hip/hip_runtime.h>
@@ -97,19 +99,37 @@ int main() {
   HIP_OK(hipMalloc((void**)&row_idx, (size_t)(nnz > 0 ? nnz : 1) * 4));
   GKI_OK(gki_block_list_fill(tiles, nqt, nkt, row_ptr, col_ptr, row_idx, nullptr, stream));
 
+  // the workgroup order (heaviest q tiles first on each XCD), from a host copy
+  // of the row pointers
+  std::vector<int32_t> h_row_ptr(nqt + 1), h_order((size_t)nqt * B * H);
+  HIP_OK(hipMemcpy(h_row_ptr.data(), row_ptr, (nqt + 1) * 4, hipMemcpyDeviceToHost));
+  GKI_OK(gki_fwd_order(h_row_ptr.data(), nqt, B * H, h_order.data()));
+  int32_t* order;
+  HIP_OK(hipMalloc((void**)&order, h_order.size() * 4));
+  HIP_OK(hipMemcpy(order, h_order.data(), h_order.size() * 4, hipMemcpyHostToDevice));
+
   // a schedule for another tile count is rejected before anything launches
-  if (gki_bsa_fwd(q, k, v, o, lse, 2, B, H, H, N, N, D, row_ptr, row_idx, nqt + 1, mask, nqb, nkb, BM,
-                  BN, scale, 1, S, W, stream) == 0) {
+  if (gki_bsa_fwd(q, k, v, o, lse, 2, B, H, H, N, N, D, row_ptr, row_idx, nqt + 1, order, mask, nqb,
+                  nkb, BM, BN, scale, 1, S, W, stream) == 0) {
     std::fprintf(stderr, "a wrong-size schedule was accepted\n");
     return 4;
   }
-  GKI_OK(gki_bsa_fwd(q, k, v, o, lse, 2, B, H, H, N, N, D, row_ptr, row_idx, nqt, mask, nqb, nkb, BM, BN,
-                     scale, 1, S, W, stream));
-  std::vector<uint16_t> ho(elems);
-  std::vector<float> hl((size_t)B * H * N);
+  GKI_OK(gki_bsa_fwd(q, k, v, o, lse, 2, B, H, H, N, N, D, row_ptr, row_idx, nqt, order, mask, nqb, nkb,
+                     BM, BN, scale, 1, S, W, stream));
+  std::vector<uint16_t> ho(elems), ho_idx(elems);
+  std::vector<float> hl((size_t)B * H * N), hl_idx(hl.size());
   HIP_OK(hipMemcpyAsync(ho.data(), o, elems * 2, hipMemcpyDeviceToHost, stream));
   HIP_OK(hipMemcpyAsync(hl.data(), lse, hl.size() * 4, hipMemcpyDeviceToHost, stream));
+  // the same launch in index order (no table) gives the same bits
+  GKI_OK(gki_bsa_fwd(q, k, v, o, lse, 2, B, H, H, N, N, D, row_ptr, row_idx, nqt, nullptr, mask, nqb, nkb,
+                     BM, BN, scale, 1, S, W, stream));
+  HIP_OK(hipMemcpyAsync(ho_idx.data(), o, elems * 2, hipMemcpyDeviceToHost, stream));
+  HIP_OK(hipMemcpyAsync(hl_idx.data(), lse, hl.size() * 4, hipMemcpyDeviceToHost, stream));
   HIP_OK(hipStreamSynchronize(stream));
+  if (ho != ho_idx || std::memcmp(hl.data(), hl_idx.data(), hl.size() * 4) != 0) {
+    std::fprintf(stderr, "the ordered launch differs from the index-order launch\n");
+    return 5;
+  }
 
   // host reference: softmax over the keys the token rule leaves each row
   // (k <= q and (k < S or k >= q - W + 1); the streaming block mask keeps a
@@ -151,7 +171,7 @@ int main() {
   std::printf("abi %d, %d kept forward tiles: max |dO| %.3e, max |dLSE| %.3e, %d out of tolerance\n",
               gki_abi_version(), nnz, max_o, max_lse, bad);
   for (void* p : {q, k, v, o, (void*)lse, (void*)mask, (void*)tiles, (void*)rc, (void*)cc,
-                  (void*)row_ptr, (void*)col_ptr, (void*)row_idx})
+                  (void*)row_ptr, (void*)col_ptr, (void*)row_idx, (void*)order})
     HIP_OK(hipFree(p));
   HIP_OK(hipStreamDestroy(stream));
   if (bad) return 1;

@@ -20,7 +20,7 @@ import torch
 import fx_compiler_pass as fxp
 import sparse_triton_kernel as stk
 from gki import _lib, build_block_lists
-from gki.lists import bwd_schedule, decode_schedule, fwd_schedule
+from gki.lists import bwd_schedule, decode_schedule, fwd_order, fwd_schedule
 from oracle import chunked_reference as cr
 from oracle import streaming_oracle as so
 
@@ -495,6 +495,48 @@ def test_config5_layer_bf16_full():
     _close(out, ref[0], torch.bfloat16, "c5 O")
     for name, t, r in zip(("dQ", "dK", "dV"), leaves, ref[2:]):
         _close(t.grad, r, torch.bfloat16, f"c5 {name}")
+
+
+@pytest.mark.parametrize("B,H,H_kv,N,D,dtype", [
+    (1, 3, 3, 300, 64, torch.bfloat16),       # 9 units: XCD shares of 2 and 1
+    (2, 8, 2, 1000, 128, torch.float16),      # grouped-query, ragged last tile
+    (1, 4, 4, 700, 32, torch.float32),        # the fp32 kernel's 64-row tiles
+    (4, 16, 16, 2048, 64, torch.bfloat16)])
+def test_fwd_order_gives_the_index_order_bits(B, H, H_kv, N, D, dtype):
+    """gki_bsa_fwd with the gki_fwd_order table (what the op passes) and with
+    no table (index order) write the same O and LSE bits: each workgroup's
+    q tile is computed independently of when it runs."""
+    print(f"[case] fwd order {B}x{H}/{H_kv}x{N}x{D} {dtype}", flush=True)
+    S, W, bm = 4, 256, 64
+    q, k, v, _ = _inputs((B, H, N, D), (B, H_kv, N, D), dtype, seed=17)
+    mask = stk.make_streaming_mask(N, N, stk.StreamingMaskSpec(S, W), bm, bm, device=DEV)
+    fp32 = dtype == torch.float32
+    sched = fwd_schedule(mask, N, N, bm, bm, True, S, W, fp32)
+    order = fwd_order(mask, sched, B * H)
+    assert sorted(order.cpu().tolist()) == list(range(sched.n_qt * B * H))
+    code = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}[dtype]
+    n_b = (N + bm - 1) // bm
+    lib = _lib.load()
+    outs = []
+    for table in (order.data_ptr(), None):
+        o, lse = torch.empty_like(q), torch.empty((B, H, N), dtype=torch.float32, device=DEV)
+        rc = lib.gki_bsa_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                             code, B, H, H_kv, N, N, D, sched.lists.row_ptr.data_ptr(),
+                             sched.lists.row_buf.data_ptr(), sched.n_qt, table, mask.data_ptr(),
+                             n_b, n_b, bm, bm, 1.0 / math.sqrt(D), 1, S, W,
+                             torch.cuda.current_stream().cuda_stream)
+        assert rc == 0, lib.gki_last_error()
+        outs.append((o, lse))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    if B * H * N * N > 2e7:          # bits only: the dense fp64 oracle would hold GBs of scores
+        return
+    eff = so.effective_mask(mask.cpu().numpy(), N, N, bm, bm, True, S, W)
+    group = H // H_kv
+    qn, kn, vn = (t.to(torch.float64).cpu().numpy() for t in (q, k, v))
+    o_ref, _ = so.attention_fwd(qn, so.expand_kv_heads(kn, group), so.expand_kv_heads(vn, group), eff,
+                                1.0 / math.sqrt(D))
+    _close(outs[0][0], torch.from_numpy(o_ref), dtype, "O with the order table")
 
 
 def test_fwd_bwd_deterministic():

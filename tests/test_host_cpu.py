@@ -104,7 +104,7 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(lib, name), f"{name} declared in gki_bsa.h but not exported"
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
     assert set(_lib.SIGNATURES) == set(names)
-    assert lib.gki_abi_version() == 4
+    assert lib.gki_abi_version() == 5
 
 
 def test_dkdv_work_list_matches_oracle():
@@ -135,6 +135,47 @@ def test_dkdv_work_list_matches_oracle():
             np.testing.assert_array_equal(split.numpy()[:n_split], want_split)
             if max_chunk > 0:
                 assert (want_items[:, 2] - want_items[:, 1]).max(initial=0) <= max_chunk
+
+
+def test_fwd_order_sorts_each_xcd_share_heaviest_first():
+    """gki_fwd_order (host code): a permutation of the n_qt * bh work units that
+    keeps each XCD's share (the hardware hands workgroup b to XCD b % 8, so XCD
+    x runs n // 8 units, one more for x < n % 8, as one contiguous range of
+    logical ids in XCD order) and sorts every share by descending kept-tile
+    count, ties in unit order -- which fixes the table uniquely."""
+    lib = _lib.load()
+    rng = np.random.default_rng(5)
+    cases = [(np.array([0, 3]), 1), (np.array([0, 0, 0]), 5)]
+    # the c2 forward schedule's row lengths (sink + window tiles, light first rows)
+    lens = np.minimum(np.arange(128) * 2 + 2, 34)
+    cases.append((np.concatenate([[0], np.cumsum(lens)]), 32))
+    for _ in range(30):
+        n_qt = int(rng.integers(1, 300))
+        cnt = rng.integers(0, 6, n_qt) * int(rng.choice([1, 7]))
+        cases.append((np.concatenate([[0], np.cumsum(cnt)]), int(rng.choice([1, 3, 8, 13, 64]))))
+    for row_ptr, bh in cases:
+        row_ptr = np.ascontiguousarray(row_ptr, dtype=np.int32)
+        n_qt = len(row_ptr) - 1
+        n = n_qt * bh
+        order = np.full(n, -1, dtype=np.int32)
+        assert lib.gki_fwd_order(row_ptr.ctypes.data, n_qt, bh, order.ctypes.data) == 0
+        assert np.array_equal(np.sort(order), np.arange(n))
+        length = np.diff(row_ptr)[order % n_qt]
+        lo = 0
+        for x in range(8):
+            hi = lo + n // 8 + (x < n % 8)
+            share = order[lo:hi]
+            assert np.array_equal(np.sort(share), np.arange(lo, hi)), "a unit left its XCD"
+            d_len, d_id = np.diff(length[lo:hi]), np.diff(share)
+            assert (d_len <= 0).all() and (d_id[d_len == 0] > 0).all()
+            lo = hi
+        assert lo == n
+    bad = np.array([0, 4, 2], dtype=np.int32)
+    out = np.zeros(4, dtype=np.int32)
+    assert lib.gki_fwd_order(bad.ctypes.data, 2, 2, out.ctypes.data) == 1
+    assert b"non-decreasing" in lib.gki_last_error()
+    assert lib.gki_fwd_order(bad.ctypes.data, 0, 2, out.ctypes.data) == 1
+    assert lib.gki_fwd_order(None, 2, 2, out.ctypes.data) == 1
 
 
 def test_decode_routing_rules():
@@ -208,19 +249,19 @@ def test_capi_rejects_bad_arguments_before_launch():
     lib = _lib.load()
     null = ctypes.c_void_p(0)
     # unsupported head_dim: code 2, nothing launched
-    rc = lib.gki_bsa_fwd(1, 1, 1, 1, 1, 2, 1, 1, 1, 64, 64, 48, 1, 1, 1, 1, 1, 1, 64, 64, 0.1, 1, 4, 8,
+    rc = lib.gki_bsa_fwd(1, 1, 1, 1, 1, 2, 1, 1, 1, 64, 64, 48, 1, 1, 1, 0, 1, 1, 1, 64, 64, 0.1, 1, 4, 8,
                          null)
     assert rc == 2 and b"head_dim" in lib.gki_last_error()
     # bad dtype code
-    rc = lib.gki_bsa_fwd(1, 1, 1, 1, 1, 7, 1, 1, 1, 64, 64, 64, 1, 1, 1, 1, 1, 1, 64, 64, 0.1, 1, 4, 8,
+    rc = lib.gki_bsa_fwd(1, 1, 1, 1, 1, 7, 1, 1, 1, 64, 64, 64, 1, 1, 1, 0, 1, 1, 1, 64, 64, 0.1, 1, 4, 8,
                          null)
     assert rc == 2 and b"dtype" in lib.gki_last_error()
     # mask shape mismatch
-    rc = lib.gki_bsa_fwd(1, 1, 1, 1, 1, 0, 1, 1, 1, 64, 64, 64, 1, 1, 1, 1, 2, 1, 64, 64, 0.1, 1, 4, 8,
+    rc = lib.gki_bsa_fwd(1, 1, 1, 1, 1, 0, 1, 1, 1, 64, 64, 64, 1, 1, 1, 0, 1, 2, 1, 64, 64, 0.1, 1, 4, 8,
                          null)
     assert rc == 1 and b"mask shape" in lib.gki_last_error()
     # schedule row count mismatch
-    rc = lib.gki_bsa_fwd(16, 16, 16, 16, 16, 0, 1, 1, 1, 200, 64, 64, 16, 16, 2, 1, 4, 1, 64, 64,
+    rc = lib.gki_bsa_fwd(16, 16, 16, 16, 16, 0, 1, 1, 1, 200, 64, 64, 16, 16, 2, 0, 1, 4, 1, 64, 64,
                          0.1, 1, 4, 8, null)
     assert rc == 1 and b"schedule" in lib.gki_last_error()
     # decode: too many rows
@@ -237,15 +278,15 @@ def test_capi_rejects_bad_arguments_before_launch():
                             0.1, 1, 4, 8, 0, 2, null)
     assert rc == 1 and b"workspace" in lib.gki_last_error()
     # misaligned tensor pointers are rejected before any launch
-    rc = lib.gki_bsa_fwd(16, 18, 16, 16, 16, 2, 1, 1, 1, 64, 64, 64, 16, 16, 1, 16, 1, 1, 64, 64,
+    rc = lib.gki_bsa_fwd(16, 18, 16, 16, 16, 2, 1, 1, 1, 64, 64, 64, 16, 16, 1, 0, 16, 1, 1, 64, 64,
                          0.1, 1, 4, 8, null)
     assert rc == 1 and b"aligned" in lib.gki_last_error()
     # grouped-query attention: H_kv must divide H
-    rc = lib.gki_bsa_fwd(1, 1, 1, 1, 1, 2, 1, 6, 4, 64, 64, 64, 1, 1, 1, 1, 1, 1, 64, 64, 0.1, 1, 4,
+    rc = lib.gki_bsa_fwd(1, 1, 1, 1, 1, 2, 1, 6, 4, 64, 64, 64, 1, 1, 1, 0, 1, 1, 1, 64, 64, 0.1, 1, 4,
                          8, null)
     assert rc == 1 and b"H_kv" in lib.gki_last_error()
     # a block mask of 2^31 or more entries (kernels index it with 32-bit offsets)
     n = 1 << 20
-    rc = lib.gki_bsa_fwd(16, 16, 16, 16, 16, 2, 1, 1, 1, n, n, 64, 16, 16, 1, 16, n // 16, n // 16, 16,
+    rc = lib.gki_bsa_fwd(16, 16, 16, 16, 16, 2, 1, 1, 1, n, n, 64, 16, 16, 1, 0, 16, n // 16, n // 16, 16,
                          16, 0.1, 1, 4, 8, null)
     assert rc == 1 and b"block mask too large" in lib.gki_last_error()
