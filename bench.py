@@ -103,6 +103,36 @@ def _time_calls(fn, steps: int, warmup: int):
     return per_step, [a.elapsed_time(b) for a, b in evs]
 
 
+def _time_fwd_bwd(fwd, step, steps: int, warmup: int):
+    """Forward and backward time of a training step, each as back-to-back
+    work between one pair of HIP events: ``steps`` forwards (``fwd``, its
+    output dropped), then ``steps`` full steps (``step``: forward, backward);
+    backward = step - forward. An event recorded between the two phases of
+    every step would put a queue drain (~10-30 us on this stack) inside each
+    phase. Returns (fwd ms, bwd ms, step ms, host wall ms per step)."""
+    import torch
+
+    _warm(step, warmup)
+
+    def loop(fn):
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        w0 = time.perf_counter()
+        t0.record()
+        for _ in range(steps):
+            fn()
+        t1.record()
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) / steps, (time.perf_counter() - w0) * 1e3 / steps
+
+    fwd_ms, _ = loop(fwd)
+    step_ms, wall = loop(step)
+    return fwd_ms, step_ms - fwd_ms, step_ms, wall
+
+
+TRAIN_TIMING = ("back-to-back between one pair of HIP events: fwd = --steps forwards, "
+                "step = --steps fwd+bwd steps, bwd = step - fwd")
+
+
 def _time_cold(fn, calls: int = 40):
     """Per-call time of ``fn`` with the device's last-level (Infinity) cache
     evicted first: a 2 GiB read runs before each timed call (outside its
@@ -190,31 +220,20 @@ def section_c3(steps: int, warmup: int, cpu_sample: Optional[dict] = None) -> di
     kept = int(mask.sum().item())
     f_fwd = 4.0 * bm * bm * D * kept * B * H
     f_bwd = 10.0 * bm * bm * D * kept * B * H
-    evs = []
 
-    def one():
+    def forward():
+        return stk.block_sparse_attention(q, k, v, mask, is_causal=True, sink_size=S, window_size=W)
+
+    def step():
         for t in (q, k, v):
             t.grad = None
-        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
-        e[0].record()
-        out = stk.block_sparse_attention(q, k, v, mask, is_causal=True, sink_size=S, window_size=W)
-        e[1].record()
-        out.backward(do)
-        e[2].record()
-        evs.append(e)
+        forward().backward(do)
 
-    _warm(one, warmup)
-    evs.clear()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        one()
-    torch.cuda.synchronize()
-    wall = (time.perf_counter() - t0) * 1e3 / steps
-    fwd = statistics.mean(e[0].elapsed_time(e[1]) for e in evs)
-    bwd = statistics.mean(e[1].elapsed_time(e[2]) for e in evs)
+    fwd, bwd, step_ms, wall = _time_fwd_bwd(forward, step, steps, warmup)
     res = {
         "workload": "c3 training fwd+bwd: B4 H16 N8192 D64 fp16, S4 W1024, 64x64 blocks, causal",
-        "kept_tiles": kept, "fwd_ms": fwd, "bwd_ms": bwd, "ms_per_step": wall,
+        "kept_tiles": kept, "fwd_ms": fwd, "bwd_ms": bwd, "ms_per_step": step_ms,
+        "host_wall_ms_per_step": wall, "timing": TRAIN_TIMING,
         "fwd_tflops": f_fwd / (fwd * 1e-3) / 1e12, "bwd_tflops": f_bwd / (bwd * 1e-3) / 1e12,
         "fwdbwd_tflops": (f_fwd + f_bwd) / ((fwd + bwd) * 1e-3) / 1e12,
     }
@@ -352,30 +371,21 @@ def section_c5(steps: int, warmup: int) -> dict:
     kept = int(mask.sum().item())
     f_fwd = 4.0 * bm * bn * D * kept * B * H
     f_bwd = 10.0 * bm * bn * D * kept * B * H
-    evs = []
 
-    def one():
+    def forward():
+        return stk.block_sparse_attention(q, k, v, mask, block_m=bm, block_n=bn, is_causal=True,
+                                          sink_size=S, window_size=W)
+
+    def step():
         for t in (q, k, v):
             t.grad = None
-        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
-        e[0].record()
-        out = stk.block_sparse_attention(q, k, v, mask, block_m=bm, block_n=bn, is_causal=True,
-                                         sink_size=S, window_size=W)
-        e[1].record()
-        out.backward(do)
-        e[2].record()
-        evs.append(e)
+        forward().backward(do)
 
-    _warm(one, warmup)
-    evs.clear()
-    for _ in range(steps):
-        one()
-    torch.cuda.synchronize()
-    fwd = statistics.mean(e[0].elapsed_time(e[1]) for e in evs)
-    bwd = statistics.mean(e[1].elapsed_time(e[2]) for e in evs)
+    fwd, bwd, step_ms, wall = _time_fwd_bwd(forward, step, steps, warmup)
     res = {
         "workload": "c5 attention layer fwd+bwd: B1 H16 N131072 D64 bf16, S4 W4096, 128x64 blocks",
-        "kept_tiles": kept, "fwd_ms": fwd, "bwd_ms": bwd,
+        "kept_tiles": kept, "fwd_ms": fwd, "bwd_ms": bwd, "ms_per_step": step_ms,
+        "host_wall_ms_per_step": wall, "timing": TRAIN_TIMING,
         "fwd_tflops": f_fwd / (fwd * 1e-3) / 1e12, "bwd_tflops": f_bwd / (bwd * 1e-3) / 1e12,
         "fwdbwd_tflops": (f_fwd + f_bwd) / ((fwd + bwd) * 1e-3) / 1e12,
         "attention_ms_12_layers": 12 * (fwd + bwd),
