@@ -283,6 +283,7 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
       floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
       floatx4 dp = floatx4{ndl4.x, ndl4.y, ndl4.z, ndl4.w};
       const int r = rho(t, col);
+      mfma_priority_hi<(D <= 64)>();
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         const int d0 = 32 * ks + 8 * grp;
@@ -291,6 +292,7 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
         s = T::mfma(aq, kf[ks], s);
         dp = T::mfma(ad, vf[ks], dp);
       }
+      mfma_priority_lo<(D <= 64)>();
       const float lv[4] = {lse4.x, lse4.y, lse4.z, lse4.w};          // base-2 LSE
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -312,6 +314,7 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
           ds[t][i] = vis.pick(t, i, ds[t][i], 0.f);
         }
     }
+    mfma_priority_hi<(D <= 64)>();
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
       const uint4 ap = pack8<T>(p[2 * st], p[2 * st + 1]);
@@ -322,6 +325,7 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
         dk[dt] = T::mfma(ad, lds_tr8<D>(cq, 32 * st, 16 * dt, lane), dk[dt]);
       }
     }
+    mfma_priority_lo<(D <= 64)>();
     dma_wait();        // the next tile's LDS-DMA has landed before the barrier
     __syncthreads();
   }
@@ -605,6 +609,7 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_16(
       floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
       floatx4 dp = floatx4{ndlt, ndlt, ndlt, ndlt};
       const int r = rho(t, col);
+      mfma_priority_hi<(D <= 64)>();
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         const int d0 = 32 * ks + 8 * grp;
@@ -613,6 +618,7 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_16(
         s = T::mfma(ak, qf[ks], s);
         dp = T::mfma(av, df[ks], dp);
       }
+      mfma_priority_lo<(D <= 64)>();
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], g.scale_log2, -lse2));
@@ -626,12 +632,14 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_16(
 #pragma unroll
         for (int i = 0; i < 4; ++i) ds[t][i] = vis.pick(t, i, ds[t][i], 0.f);
     }
+    mfma_priority_hi<(D <= 64)>();
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
       const uint4 b = pack8<T>(ds[2 * st], ds[2 * st + 1]);
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) dq[dt] = T::mfma(lds_tr8<D>(ck, 32 * st, 16 * dt, lane), b, dq[dt]);
     }
+    mfma_priority_lo<(D <= 64)>();
     dma_wait();        // the next tile's LDS-DMA has landed before the barrier
     __syncthreads();
   }

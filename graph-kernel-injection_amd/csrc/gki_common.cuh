@@ -518,6 +518,21 @@ __host__ __device__ inline int xcd_start(int x, int n) {
 }
 __host__ __device__ inline int xcd_remap(int b, int n) { return xcd_start(b % kXcd, n) + b / kXcd; }
 
+// Wave issue priority around a cluster of MFMAs (ON: the D <= 64 kernels).
+// While a wave issues its products it wins the SIMD's issue arbitration over
+// the waves in their softmax / dS VALU phase, so the matrix pipe is fed more
+// evenly: forward -2%, backward -0.5 to -1.3% at D = 64 (c3, c5); at
+// D = 128 (two waves per SIMD) it made the forward 3% slower, so it is off
+// there.
+template <bool ON>
+__device__ inline void mfma_priority_hi() {
+  if constexpr (ON) __builtin_amdgcn_s_setprio(1);
+}
+template <bool ON>
+__device__ inline void mfma_priority_lo() {
+  if constexpr (ON) __builtin_amdgcn_s_setprio(0);
+}
+
 // Work unit of workgroup b in a launch over n units: its XCD-remapped logical
 // id, or, with an order table (gki_fwd_order), the unit that table lists at
 // that id (each XCD's range sorted heaviest first, so the units dispatched last

@@ -145,6 +145,7 @@ __global__ __launch_bounds__(kFwdThreads, D <= 64 ? 4 : 2) void fwd_kernel_16(
     const uint16_t* cv = sv[buf];
 
     floatx4 s[RB][4];
+    mfma_priority_hi<(D <= 64)>();
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
 #pragma unroll
@@ -159,6 +160,7 @@ __global__ __launch_bounds__(kFwdThreads, D <= 64 ? 4 : 2) void fwd_kernel_16(
       }
     }
 
+    mfma_priority_lo<(D <= 64)>();
 #pragma unroll
     for (int h = 0; h < RB; ++h) {
       const int q0 = qw + 16 * h;
@@ -197,6 +199,7 @@ __global__ __launch_bounds__(kFwdThreads, D <= 64 ? 4 : 2) void fwd_kernel_16(
           s[h][t][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[h][t][i], g.qk_scale_log2, -m[h]));
     }
 
+    mfma_priority_hi<(D <= 64)>();
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
       uint4 b[RB];
@@ -211,6 +214,7 @@ __global__ __launch_bounds__(kFwdThreads, D <= 64 ? 4 : 2) void fwd_kernel_16(
 #pragma unroll
       for (int h = 0; h < RB; ++h) lsum[h] = T::mfma(ones, b[h], lsum[h]);
     }
+    mfma_priority_lo<(D <= 64)>();
     dma_wait();        // the next tile's LDS-DMA has landed before the barrier
     __syncthreads();
   }
