@@ -772,7 +772,10 @@ int launch_decode_mfma(const Geom& g, const void* q, const void* k, const void* 
     }
   }
   const int n_rows = g.group * g.n_q;
-#define GKI_MFMA_DECODE(EX, NBK)                                                                    hipLaunchKernelGGL((decode_mfma_kernel<T, D, EX, NBK>), dim3(n_wgh * n_splits), dim3(256), lds,                       stream, g, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,                             (uint16_t*)o, lse, ws, src, kv_rows, n_tokens, n_splits)
+#define GKI_MFMA_DECODE(EX, NBK)                                                            \
+  hipLaunchKernelGGL((decode_mfma_kernel<T, D, EX, NBK>), dim3(n_wgh * n_splits), dim3(256), lds, \
+                     stream, g, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,      \
+                     (uint16_t*)o, lse, ws, src, kv_rows, n_tokens, n_splits)
   if (n_rows <= kDecodeTileM) {
     if (g.n_q == 1) GKI_MFMA_DECODE(true, 1);
     else GKI_MFMA_DECODE(false, 1);
@@ -879,11 +882,14 @@ int decode_ring_dispatch(int dtype, int head_dim, const Geom& g, const void* q, 
   src.ring = ring;
   if (decode_on_mfma(dtype, head_dim, g)) {
     const char* what = "gki_rolling_decode";
+    const int rows = g.sink + ring;
     if (dtype == kF16)
-      return head_dim == 64 ? launch_decode_mfma<F16, 64>(g, q, k, v, o, lse, src, g.sink + ring, n_tokens, ws, n_splits, stream, what)
-                            : launch_decode_mfma<F16, 128>(g, q, k, v, o, lse, src, g.sink + ring, n_tokens, ws, n_splits, stream, what);
-    return head_dim == 64 ? launch_decode_mfma<BF16, 64>(g, q, k, v, o, lse, src, g.sink + ring, n_tokens, ws, n_splits, stream, what)
-                          : launch_decode_mfma<BF16, 128>(g, q, k, v, o, lse, src, g.sink + ring, n_tokens, ws, n_splits, stream, what);
+      return head_dim == 64
+                 ? launch_decode_mfma<F16, 64>(g, q, k, v, o, lse, src, rows, n_tokens, ws, n_splits, stream, what)
+                 : launch_decode_mfma<F16, 128>(g, q, k, v, o, lse, src, rows, n_tokens, ws, n_splits, stream, what);
+    return head_dim == 64
+               ? launch_decode_mfma<BF16, 64>(g, q, k, v, o, lse, src, rows, n_tokens, ws, n_splits, stream, what)
+               : launch_decode_mfma<BF16, 128>(g, q, k, v, o, lse, src, rows, n_tokens, ws, n_splits, stream, what);
   }
   return launch_decode(dtype, head_dim, g, q, k, v, o, lse, src, g.sink + ring, n_tokens, ws, n_splits,
                        stream, "gki_rolling_decode");

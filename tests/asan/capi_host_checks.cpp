@@ -136,24 +136,21 @@ static void check_rejections() {
     CHECK(rc != 0 && !msg.empty(), "%s: rc %d, message '%s'", what, rc, msg.c_str());
   };
   // forward: bad dtype, bad head_dim, null tensors, misaligned pointers, wrong list size
-  rejected(gki_bsa_fwd(p, p, p, p, f, 7, 1, 1, 1, 64, 64, 64, ip, ip, 1, nullptr, ip, 1, 1, 64, 64, 0.125f, 1, 4,
-                       16, nullptr), "fwd dtype 7");
-  rejected(gki_bsa_fwd(p, p, p, p, f, 2, 1, 1, 1, 64, 64, 48, ip, ip, 1, nullptr, ip, 1, 1, 64, 64, 0.125f, 1, 4,
-                       16, nullptr), "fwd head_dim 48");
-  rejected(gki_bsa_fwd(nullptr, p, p, p, f, 2, 1, 1, 1, 64, 64, 64, ip, ip, 1, nullptr, ip, 1, 1, 64, 64, 0.125f,
-                       1, 4, 16, nullptr), "fwd null q");
-  rejected(gki_bsa_fwd(buf + 2, p, p, p, f, 2, 1, 1, 1, 64, 64, 64, ip, ip, 1, nullptr, ip, 1, 1, 64, 64, 0.125f,
-                       1, 4, 16, nullptr), "fwd misaligned q");
-  rejected(gki_bsa_fwd(p, p, p, p, f, 2, 1, 1, 1, 64, 64, 64, ip, ip, 3, nullptr, ip, 1, 1, 64, 64, 0.125f, 1, 4,
-                       16, nullptr), "fwd schedule rows");
-  rejected(gki_bsa_fwd(p, p, p, p, f, 2, 1, 4, 3, 64, 64, 64, ip, ip, 1, nullptr, ip, 1, 1, 64, 64, 0.125f, 1, 4,
-                       16, nullptr), "fwd H_kv not dividing H");
-  rejected(gki_bsa_fwd(p, p, p, p, f, 2, 1, 1, 1, 64, 64, 64, ip, ip, 1, nullptr, ip, 2, 1, 64, 64, 0.125f, 1, 4,
-                       16, nullptr), "fwd mask shape");
-  rejected(gki_bsa_fwd(p, p, p, p, f, 2, 1, 1, 1, 64, 64, 64, ip, ip, 1, nullptr, ip, 1, 1, 64, 64,
-                       __builtin_inff(), 1, 4, 16, nullptr), "fwd infinite scale");
-  rejected(gki_bsa_fwd(p, p, p, p, f, 2, 1, 1, 1, 64, 64, 64, ip, ip, 1, nullptr, ip, 1, 1, 64, 64, 0.125f, 1, -1,
-                       16, nullptr), "fwd negative sink");
+  // (arguments: q, dtype, H, H_kv, head_dim, n_qt, n_qb, scale, sink; the rest fixed)
+  auto fwd = [&](void* q, int dtype, int H, int H_kv, int head_dim, int n_qt, int n_qb, float scale,
+                 int sink) {
+    return gki_bsa_fwd(q, p, p, p, f, dtype, 1, H, H_kv, 64, 64, head_dim, ip, ip, n_qt, nullptr, ip, n_qb,
+                       1, 64, 64, scale, 1, sink, 16, nullptr);
+  };
+  rejected(fwd(p, 7, 1, 1, 64, 1, 1, 0.125f, 4), "fwd dtype 7");
+  rejected(fwd(p, 2, 1, 1, 48, 1, 1, 0.125f, 4), "fwd head_dim 48");
+  rejected(fwd(nullptr, 2, 1, 1, 64, 1, 1, 0.125f, 4), "fwd null q");
+  rejected(fwd(buf + 2, 2, 1, 1, 64, 1, 1, 0.125f, 4), "fwd misaligned q");
+  rejected(fwd(p, 2, 1, 1, 64, 3, 1, 0.125f, 4), "fwd schedule rows");
+  rejected(fwd(p, 2, 4, 3, 64, 1, 1, 0.125f, 4), "fwd H_kv not dividing H");
+  rejected(fwd(p, 2, 1, 1, 64, 1, 2, 0.125f, 4), "fwd mask shape");
+  rejected(fwd(p, 2, 1, 1, 64, 1, 1, __builtin_inff(), 4), "fwd infinite scale");
+  rejected(fwd(p, 2, 1, 1, 64, 1, 1, 0.125f, -1), "fwd negative sink");
   // backward: inconsistent work list, missing partials, schedule shape
   rejected(gki_bsa_bwd(p, p, p, p, p, f, p, p, p, f, 2, 1, 1, 1, 64, 64, 64, ip, ip, 1, ip, ip, 1, ip, 0,
                        ip, 0, 0, f, ip, 1, 1, 64, 64, 0.125f, 1, 4, 16, nullptr), "bwd no items");
