@@ -539,6 +539,51 @@ def test_fwd_order_gives_the_index_order_bits(B, H, H_kv, N, D, dtype):
     _close(outs[0][0], torch.from_numpy(o_ref), dtype, "O with the order table")
 
 
+def test_fwd_order_entries_out_of_range_do_nothing():
+    """A workgroup whose order-table entry is outside 0 .. n-1 exits without
+    touching memory (the table is caller data): with every other entry
+    replaced by -5 or n, the units still listed get the bits of a full launch
+    and the rest of O / LSE keeps its sentinel."""
+    print("[case] fwd order with out-of-range entries", flush=True)
+    B, H, N, D, S, W, bm = 2, 4, 1000, 64, 4, 256, 64
+    q, k, v, _ = _inputs((B, H, N, D), (B, H, N, D), torch.bfloat16, seed=23)
+    mask = stk.make_streaming_mask(N, N, stk.StreamingMaskSpec(S, W), bm, bm, device=DEV)
+    sched = fwd_schedule(mask, N, N, bm, bm, True, S, W, False)
+    n = sched.n_qt * B * H
+    full = fwd_order(mask, sched, B * H)
+    holed = full.clone()
+    holed[0::2] = torch.tensor([-5, n], dtype=torch.int32, device=DEV).repeat(n)[: holed[0::2].numel()]
+    lib = _lib.load()
+    n_b = (N + bm - 1) // bm
+
+    def run(table):
+        o = torch.full_like(q, 0).view(torch.int16).fill_(0x7E7E).view(torch.bfloat16)
+        lse = torch.full((B, H, N), -7.0, dtype=torch.float32, device=DEV)
+        rc = lib.gki_bsa_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                             2, B, H, H, N, N, D, sched.lists.row_ptr.data_ptr(),
+                             sched.lists.row_buf.data_ptr(), sched.n_qt, table.data_ptr(),
+                             mask.data_ptr(), n_b, n_b, bm, bm, 1.0 / math.sqrt(D), 1, S, W,
+                             torch.cuda.current_stream().cuda_stream)
+        assert rc == 0, lib.gki_last_error()
+        return o, lse
+
+    o_full, l_full = run(full)
+    o_hole, l_hole = run(holed)
+    torch.cuda.synchronize()
+    kept = set(full[1::2].tolist())
+    tm = _lib.tile_sizes()["fwd_tile_m_16"]
+    for unit in range(n):
+        bh, qt = divmod(unit, sched.n_qt)
+        b, h = divmod(bh, H)
+        rows = slice(qt * tm, min(N, (qt + 1) * tm))
+        if unit in kept:
+            assert torch.equal(o_hole[b, h, rows], o_full[b, h, rows]), unit
+            assert torch.equal(l_hole[b, h, rows], l_full[b, h, rows]), unit
+        else:
+            assert (o_hole[b, h, rows].view(torch.int16) == 0x7E7E).all(), unit
+            assert (l_hole[b, h, rows] == -7.0).all(), unit
+
+
 def test_fwd_bwd_deterministic():
     B, H, N, D, S, W = 2, 4, 2048, 64, 4, 256
     q, k, v, do = _inputs((B, H, N, D), (B, H, N, D), torch.bfloat16, seed=9, grad_out=True)
