@@ -518,7 +518,8 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_16(
     Geom g, const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const uint16_t* __restrict__ V, const uint16_t* __restrict__ O, const uint16_t* __restrict__ dO,
     uint16_t* __restrict__ dQ, const float* __restrict__ LSE, float* __restrict__ Delta,
-    const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ row_idx, int n_qt) {
+    const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ row_idx, int n_qt,
+    const int32_t* __restrict__ dq_order) {
   constexpr int KS = (D + 31) / 32;
   constexpr int DT = D / 16;
   using Tile = RowTile<D>;
@@ -526,7 +527,8 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_16(
   __shared__ __align__(16) uint16_t sv[2][64 * D];
 
   const int n_wg = n_qt * g.B * g.H;
-  const int wg = xcd_remap(blockIdx.x, n_wg);
+  const int wg = work_of(blockIdx.x, n_wg, dq_order);
+  if (wg < 0) return;
   const int bh = wg / n_qt, qt = wg - bh * n_qt;
   const size_t qb = (size_t)bh * g.n_q * D;
   const size_t kb = (size_t)kv_bh(g, bh) * g.n_kv * D;
@@ -669,7 +671,7 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_32(
     Geom g, const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ dO, float* __restrict__ dQ, const float* __restrict__ LSE,
     const float* __restrict__ Delta, const int32_t* __restrict__ row_ptr,
-    const int32_t* __restrict__ row_idx, int n_qt) {
+    const int32_t* __restrict__ row_idx, int n_qt, const int32_t* __restrict__ dq_order) {
   constexpr int KS = D / 4;
   constexpr int DT = D / 16;
   constexpr int LD = D + 4;
@@ -677,7 +679,8 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_32(
   Stage32<D> sk, sv;
 
   const int n_wg = n_qt * g.B * g.H;
-  const int wg = xcd_remap(blockIdx.x, n_wg);
+  const int wg = work_of(blockIdx.x, n_wg, dq_order);
+  if (wg < 0) return;
   const int bh = wg / n_qt, qt = wg - bh * n_qt;
   const size_t qb = (size_t)bh * g.n_q * D;
   const size_t kb = (size_t)kv_bh(g, bh) * g.n_kv * D;
@@ -768,12 +771,12 @@ void launch_delta(const void* o, const void* dout, float* delta, int64_t rows, h
 template <typename T, int D, bool DEFER>
 void launch_bwd16_as(const Geom& g, const void* q, const void* k, const void* v, const void* o,
                      const void* dout, const float* lse, void* dq, void* dk, void* dv, float* delta,
-                     const int32_t* row_ptr, const int32_t* row_idx, int n_qt, const int32_t* col_ptr,
-                     const int32_t* col_idx, const KvWork& w, hipStream_t stream) {
+                     const int32_t* row_ptr, const int32_t* row_idx, int n_qt, const int32_t* dq_order,
+                     const int32_t* col_ptr, const int32_t* col_idx, const KvWork& w, hipStream_t stream) {
   const int BH = g.B * g.H, BHkv = g.B * g.H_kv;
   hipLaunchKernelGGL((dq_kernel_16<T, D, DEFER>), dim3(n_qt * BH), dim3(256), 0, stream, g,
                      (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)o,
-                     (const uint16_t*)dout, (uint16_t*)dq, lse, delta, row_ptr, row_idx, n_qt);
+                     (const uint16_t*)dout, (uint16_t*)dq, lse, delta, row_ptr, row_idx, n_qt, dq_order);
   hipLaunchKernelGGL((dkdv_kernel_16<T, D, DEFER>), dim3(w.n_items * BHkv), dim3(256), 0, stream, g,
                      (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)dout,
                      (uint16_t*)dk, (uint16_t*)dv, lse, delta, col_ptr, col_idx, w);
@@ -782,21 +785,21 @@ void launch_bwd16_as(const Geom& g, const void* q, const void* k, const void* v,
 template <typename T, int D>
 void launch_bwd16(const Geom& g, const void* q, const void* k, const void* v, const void* o,
                   const void* dout, const float* lse, void* dq, void* dk, void* dv, float* delta,
-                  const int32_t* row_ptr, const int32_t* row_idx, int n_qt, const int32_t* col_ptr,
-                  const int32_t* col_idx, const KvWork& w, hipStream_t stream) {
+                  const int32_t* row_ptr, const int32_t* row_idx, int n_qt, const int32_t* dq_order,
+                  const int32_t* col_ptr, const int32_t* col_idx, const KvWork& w, hipStream_t stream) {
   if (g.defer_scale)
     launch_bwd16_as<T, D, true>(g, q, k, v, o, dout, lse, dq, dk, dv, delta, row_ptr, row_idx, n_qt,
-                                col_ptr, col_idx, w, stream);
+                                dq_order, col_ptr, col_idx, w, stream);
   else
     launch_bwd16_as<T, D, false>(g, q, k, v, o, dout, lse, dq, dk, dv, delta, row_ptr, row_idx, n_qt,
-                                 col_ptr, col_idx, w, stream);
+                                 dq_order, col_ptr, col_idx, w, stream);
 }
 
 template <int D>
 int launch_bwd(int dtype, const Geom& g, const void* q, const void* k, const void* v, const void* o,
                const void* dout, const float* lse, void* dq, void* dk, void* dv, float* delta,
-               const int32_t* row_ptr, const int32_t* row_idx, int n_qt, const int32_t* col_ptr,
-               const int32_t* col_idx, const KvWork& w, hipStream_t stream) {
+               const int32_t* row_ptr, const int32_t* row_idx, int n_qt, const int32_t* dq_order,
+               const int32_t* col_ptr, const int32_t* col_idx, const KvWork& w, hipStream_t stream) {
   const int BH = g.B * g.H, BHkv = g.B * g.H_kv;
   const int64_t rows = (int64_t)BH * g.n_q;
   const dim3 kv_grid(w.n_items * BHkv), red_grid(w.n_split * BHkv * kReduceWgPerTile<D>);
@@ -810,16 +813,16 @@ int launch_bwd(int dtype, const Geom& g, const void* q, const void* k, const voi
                          (float*)dk, (float*)dv);
     hipLaunchKernelGGL(dq_kernel_32<D>, dim3(n_qt * BH), dim3(256), 0, stream, g, (const float*)q,
                        (const float*)k, (const float*)v, (const float*)dout, (float*)dq, lse, delta,
-                       row_ptr, row_idx, n_qt);
+                       row_ptr, row_idx, n_qt, dq_order);
   } else if (dtype == kF16) {
     launch_bwd16<F16, D>(g, q, k, v, o, dout, lse, dq, dk, dv, delta, row_ptr, row_idx, n_qt,
-                         col_ptr, col_idx, w, stream);
+                         dq_order, col_ptr, col_idx, w, stream);
     if (w.n_split > 0)
       hipLaunchKernelGGL((dkdv_reduce_kernel<F16, D>), red_grid, dim3(256), 0, stream, g, w,
                          (uint16_t*)dk, (uint16_t*)dv);
   } else {
     launch_bwd16<BF16, D>(g, q, k, v, o, dout, lse, dq, dk, dv, delta, row_ptr, row_idx, n_qt,
-                         col_ptr, col_idx, w, stream);
+                          dq_order, col_ptr, col_idx, w, stream);
     if (w.n_split > 0)
       hipLaunchKernelGGL((dkdv_reduce_kernel<BF16, D>), red_grid, dim3(256), 0, stream, g, w,
                          (uint16_t*)dk, (uint16_t*)dv);
@@ -832,11 +835,12 @@ int launch_bwd(int dtype, const Geom& g, const void* q, const void* k, const voi
 int bwd_dispatch(int dtype, int head_dim, const Geom& g, const void* q, const void* k, const void* v,
                  const void* o, const void* dout, const float* lse, void* dq, void* dk, void* dv,
                  float* delta, const int32_t* row_ptr, const int32_t* row_idx, int n_qt,
-                 const int32_t* col_ptr, const int32_t* col_idx, const KvWork& w, hipStream_t stream) {
+                 const int32_t* dq_order, const int32_t* col_ptr, const int32_t* col_idx, const KvWork& w,
+                 hipStream_t stream) {
 #define GKI_BWD_CASE(DD)                                                                          \
   case DD:                                                                                        \
     return launch_bwd<DD>(dtype, g, q, k, v, o, dout, lse, dq, dk, dv, delta, row_ptr, row_idx,   \
-                          n_qt, col_ptr, col_idx, w, stream);
+                          n_qt, dq_order, col_ptr, col_idx, w, stream);
   switch (head_dim) {
     GKI_BWD_CASE(16)
     GKI_BWD_CASE(32)

@@ -38,7 +38,8 @@ int fwd_dispatch(int dtype, int head_dim, const Geom& g, const void* q, const vo
 int bwd_dispatch(int dtype, int head_dim, const Geom& g, const void* q, const void* k, const void* v,
                  const void* o, const void* dout, const float* lse, void* dq, void* dk, void* dv,
                  float* delta, const int32_t* row_ptr, const int32_t* row_idx, int n_qt,
-                 const int32_t* col_ptr, const int32_t* col_idx, const KvWork& w, hipStream_t stream);
+                 const int32_t* dq_order, const int32_t* col_ptr, const int32_t* col_idx, const KvWork& w,
+                 hipStream_t stream);
 int decode_tokens_dispatch(const Geom& g, const int32_t* list, int n_ent, int32_t* tok, int32_t* count,
                            hipStream_t stream);
 int decode_dispatch(int dtype, int head_dim, const Geom& g, const void* q, const void* k, const void* v,
@@ -205,7 +206,7 @@ using namespace gki;
 
 extern "C" {
 
-int gki_abi_version(void) { return 5; }
+int gki_abi_version(void) { return 6; }
 
 const char* gki_last_error(void) { return g_last_error.c_str(); }
 
@@ -267,9 +268,10 @@ int gki_bsa_bwd(const void* q, const void* k, const void* v, const void* o, cons
                 int32_t H, int32_t H_kv, int32_t n_q, int32_t n_kv, int32_t head_dim, const int32_t* row_ptr,
                 const int32_t* row_idx, int32_t n_qt, const int32_t* col_ptr, const int32_t* col_idx,
                 int32_t n_kt, const int32_t* kv_items, int32_t n_items, const int32_t* kv_split,
-                int32_t n_split, int32_t n_pslots, float* kv_partials, const int32_t* mask,
-                int32_t n_qb, int32_t n_kb, int32_t block_m, int32_t block_n, float softmax_scale,
-                int32_t is_causal, int32_t sink_size, int32_t window_size, void* stream) {
+                int32_t n_split, int32_t n_pslots, float* kv_partials, const int32_t* dq_order,
+                const int32_t* mask, int32_t n_qb, int32_t n_kb, int32_t block_m, int32_t block_n,
+                float softmax_scale, int32_t is_causal, int32_t sink_size, int32_t window_size,
+                void* stream) {
   Geom g;
   if (int rc = make_geom(g, dtype, B, H, H_kv, n_q, n_kv, head_dim, mask, n_qb, n_kb, block_m, block_n,
                          softmax_scale, is_causal, sink_size, window_size))
@@ -285,13 +287,14 @@ int gki_bsa_bwd(const void* q, const void* k, const void* v, const void* o, cons
               "gki_bsa_bwd: work list inconsistent with the tile count (see gki_dkdv_items)");
   GKI_REQUIRE(n_split == 0 || (kv_split && kv_partials), 1,
               "gki_bsa_bwd: split columns need kv_split and kv_partials");
+  GKI_REQUIRE((int64_t)n_qt * B * H < (1ll << 31), 1, "gki_bsa_bwd: dQ grid too large");
   GKI_REQUIRE((int64_t)n_items * B * H_kv < (1ll << 31) &&
                   (int64_t)n_split * B * H_kv * (head_dim / 8) < (1ll << 31), 1,
               "gki_bsa_bwd: dK/dV grid too large");
   GKI_REQUIRE(((uintptr_t)kv_partials & 15) == 0, 1, "gki_bsa_bwd: kv_partials must be 16-byte aligned");
   KvWork w{kv_items, n_items, kv_split, n_split, n_pslots, kv_partials};
   return bwd_dispatch(dtype, head_dim, g, q, k, v, o, dout, lse, dq, dk, dv, delta, row_ptr, row_idx,
-                      n_qt, col_ptr, col_idx, w, (hipStream_t)stream);
+                      n_qt, dq_order, col_ptr, col_idx, w, (hipStream_t)stream);
 }
 
 int gki_dkdv_items(const int32_t* col_ptr, int32_t n_kt, int32_t group, int32_t bh_kv,

@@ -39,6 +39,7 @@ SIGNATURES = {
     "gki_bsa_bwd": (ctypes.c_int, [_c_ptr] * 10 + [_c_int] * 7
                     + [_c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_int]      # CSR, CSC, n_kt
                     + [_c_ptr, _c_int, _c_ptr, _c_int, _c_int, _c_ptr]      # dK/dV work list
+                    + [_c_ptr]                                              # dQ order
                     + [_c_ptr] + [_c_int] * 4 + [_c_float] + [_c_int] * 3 + [_c_ptr]),
     "gki_bsa_decode_workspace_floats": (ctypes.c_int64, [_c_int] * 5),
     "gki_decode_tokens": (ctypes.c_int, [_c_ptr, _c_int, _c_int, _c_int, _c_ptr] + [_c_int] * 7

@@ -73,6 +73,7 @@ class BwdSchedule:
     n_pslots: int             # fp32 partial slots per (b, kv head)
     n_qt: int
     n_kt: int
+    dq_order: torch.Tensor    # [n_qt * B * H] int32, the dQ grid's workgroup order
 
 
 @dataclass(frozen=True)
@@ -264,21 +265,22 @@ def fwd_schedule(mask: torch.Tensor, n_q: int, n_kv: int, block_m: int, block_n:
     return _CACHE.get(mask, key, build)
 
 
+def _grid_order(row_ptr: torch.Tensor, n_qt: int, bh: int, device) -> torch.Tensor:
+    """``gki_fwd_order`` over a CSR's q tiles and ``bh`` = B * H heads: each
+    XCD's share of (b, h, q tile) units, longest kept-tile list first, as a
+    device int32 tensor [n_qt * bh]."""
+    lib = _lib.load()
+    host = row_ptr.to("cpu").contiguous()
+    order = torch.empty(n_qt * bh, dtype=torch.int32)
+    _lib.check(lib.gki_fwd_order(host.data_ptr(), n_qt, bh, order.data_ptr()), "gki_fwd_order")
+    return order.to(device)
+
+
 def fwd_order(mask: torch.Tensor, sched: FwdSchedule, bh: int) -> torch.Tensor:
-    """Workgroup order of the forward launch over ``bh`` = B * H heads
-    (``gki_fwd_order``: each XCD's share of (b, h, q tile) units, longest
-    kept-tile list first), a device int32 tensor [n_qt * bh], cached with the
-    schedule."""
-
-    def build() -> torch.Tensor:
-        lib = _lib.load()
-        row_ptr = sched.lists.row_ptr.to("cpu").contiguous()
-        order = torch.empty(sched.n_qt * bh, dtype=torch.int32)
-        _lib.check(lib.gki_fwd_order(row_ptr.data_ptr(), sched.n_qt, bh, order.data_ptr()),
-                   "gki_fwd_order")
-        return order.to(mask.device)
-
-    return _CACHE.get(mask, sched.key + ("order", bh), build)
+    """Workgroup order of the forward launch over ``bh`` = B * H heads,
+    cached with the schedule."""
+    return _CACHE.get(mask, sched.key + ("order", bh),
+                      lambda: _grid_order(sched.lists.row_ptr, sched.n_qt, bh, mask.device))
 
 
 def dkdv_items(col_ptr_host: torch.Tensor, group: int, bh_kv: int, max_chunk: int = 0):
@@ -316,8 +318,9 @@ def bwd_schedule(mask: torch.Tensor, n_q: int, n_kv: int, block_m: int, block_n:
         items, split, n_items, n_split, n_pslots = dkdv_items(lists.col_ptr.cpu(), group, bh_kv,
                                                               max_chunk)
         dev = mask.device
+        dq_order = _grid_order(lists.row_ptr, lists.n_rows, group * bh_kv, dev)
         return BwdSchedule(lists, items.to(dev), n_items, split.to(dev), n_split, n_pslots,
-                           lists.n_rows, lists.n_cols)
+                           lists.n_rows, lists.n_cols, dq_order)
 
     key = ("bwd", n_q, n_kv, block_m, block_n, tm, tn, bool(is_causal), sink, window, group, bh_kv,
            max_chunk)

@@ -272,7 +272,8 @@ class _BlockSparseFlashAttention(torch.autograd.Function):
                 _DTYPE_CODE[q.dtype], B, H, H_kv, N_Q, N_KV, D, L.row_ptr.data_ptr(),
                 L.row_buf.data_ptr(), sched.n_qt, L.col_ptr.data_ptr(), L.col_buf.data_ptr(),
                 sched.n_kt, sched.items.data_ptr(), sched.n_items, sched.split.data_ptr(),
-                sched.n_split, sched.n_pslots, partials.data_ptr(), block_mask.data_ptr(), n_qb,
+                sched.n_split, sched.n_pslots, partials.data_ptr(), sched.dq_order.data_ptr(),
+                block_mask.data_ptr(), n_qb,
                 n_kb, ctx.block_m, ctx.block_n, float(ctx.softmax_scale), int(ctx.is_causal),
                 ctx.sink_size, ctx.window_size, stream), "gki_bsa_bwd")
         return (dq, dk, dv) + (None,) * (7 + ctx.n_extra)

@@ -42,9 +42,9 @@
 extern "C" {
 #endif
 
-/* ABI version (currently 5: grouped-query attention, H_kv after H; dK/dV work
+/* ABI version (currently 6: grouped-query attention, H_kv after H; dK/dV work
  * items from gki_dkdv_items, whose chunk can be capped by max_chunk; the
- * forward's optional workgroup order from gki_fwd_order). */
+ * optional workgroup orders of the forward and dQ grids from gki_fwd_order). */
 int gki_abi_version(void);
 
 /* Message of the last failing call on this thread. */
@@ -112,10 +112,10 @@ int gki_dkdv_items(const int32_t* col_ptr, int32_t n_kt, int32_t group, int32_t 
                    int32_t max_chunk, int32_t* items, int32_t* n_items, int32_t* split,
                    int32_t* n_split, int32_t* n_pslots);
 
-/* Order of the forward grid's workgroups (host arrays; no reference
- * counterpart -- the reference's grid runs its programs in index order,
- * sparse_triton_kernel.py:662-682). row_ptr: the forward CSR row pointers
- * (n_qt + 1, host copy); bh: B * H. Writes order[n_qt * bh], a permutation of
+/* Order of the forward (or dQ) grid's workgroups (host arrays; no reference
+ * counterpart -- the reference's grids run their programs in index order,
+ * sparse_triton_kernel.py:662-682, 756-777). row_ptr: the forward (or
+ * backward) CSR row pointers (n_qt + 1, host copy); bh: B * H. Writes order[n_qt * bh], a permutation of
  * the work units (b * H + h) * n_qt + qt: the units each XCD receives (one
  * contiguous range per XCD, as the kernels map workgroups) sorted by
  * descending kept-tile count, ties in index order, so that each XCD ends its
@@ -144,7 +144,9 @@ int gki_bsa_fwd(const void* q, const void* k, const void* v, void* o, float* lse
  * the CSR list, both over bwd_tile_m x tile_n tiles. `delta` is a caller-owned fp32
  * [B, H, N_Q] workspace for the row terms (its contents on return are internal:
  * Delta for fp32 inputs, -Delta for fp16 / bf16). dq, dk, dv are
- * fully written (no zero-fill needed). */
+ * fully written (no zero-fill needed). dq_order: NULL (index order) or a
+ * device copy of gki_fwd_order's table for the backward CSR and B * H (the
+ * dQ grid runs each XCD's q tiles longest list first). */
 int gki_bsa_bwd(const void* q, const void* k, const void* v, const void* o,
                 const void* dout, const float* lse, void* dq, void* dk, void* dv,
                 float* delta, int32_t dtype, int32_t B, int32_t H, int32_t H_kv,
@@ -152,8 +154,8 @@ int gki_bsa_bwd(const void* q, const void* k, const void* v, const void* o,
                 const int32_t* row_idx, int32_t n_qt, const int32_t* col_ptr,
                 const int32_t* col_idx, int32_t n_kt, const int32_t* kv_items,
                 int32_t n_items, const int32_t* kv_split, int32_t n_split,
-                int32_t n_pslots, float* kv_partials, const int32_t* mask,
-                int32_t n_qb, int32_t n_kb,
+                int32_t n_pslots, float* kv_partials, const int32_t* dq_order,
+                const int32_t* mask, int32_t n_qb, int32_t n_kb,
                 int32_t block_m, int32_t block_n, float softmax_scale, int32_t is_causal,
                 int32_t sink_size, int32_t window_size, void* stream);
 

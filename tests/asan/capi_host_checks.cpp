@@ -153,12 +153,12 @@ static void check_rejections() {
   rejected(fwd(p, 2, 1, 1, 64, 1, 1, 0.125f, -1), "fwd negative sink");
   // backward: inconsistent work list, missing partials, schedule shape
   rejected(gki_bsa_bwd(p, p, p, p, p, f, p, p, p, f, 2, 1, 1, 1, 64, 64, 64, ip, ip, 1, ip, ip, 1, ip, 0,
-                       ip, 0, 0, f, ip, 1, 1, 64, 64, 0.125f, 1, 4, 16, nullptr), "bwd no items");
+                       ip, 0, 0, f, nullptr, ip, 1, 1, 64, 64, 0.125f, 1, 4, 16, nullptr), "bwd no items");
   rejected(gki_bsa_bwd(p, p, p, p, p, f, p, p, p, f, 2, 1, 1, 1, 64, 64, 64, ip, ip, 1, ip, ip, 1, ip, 2,
-                       nullptr, 1, 1, nullptr, ip, 1, 1, 64, 64, 0.125f, 1, 4, 16, nullptr),
+                       nullptr, 1, 1, nullptr, nullptr, ip, 1, 1, 64, 64, 0.125f, 1, 4, 16, nullptr),
            "bwd split without partials");
   rejected(gki_bsa_bwd(p, p, p, p, p, f, p, p, p, f, 2, 1, 1, 1, 64, 64, 64, ip, ip, 2, ip, ip, 1, ip, 1,
-                       ip, 0, 0, f, ip, 1, 1, 64, 64, 0.125f, 1, 4, 16, nullptr), "bwd schedule rows");
+                       ip, 0, 0, f, nullptr, ip, 1, 1, 64, 64, 0.125f, 1, 4, 16, nullptr), "bwd schedule rows");
   // decode: too many query rows, bad splits, missing workspace
   rejected(gki_bsa_decode(p, p, p, p, f, 2, 1, 1, 1, 5, 64, 64, ip, 1, ip, 1, 1, 64, 64, 0.125f, 1, 4,
                           16, f, 1, nullptr), "decode n_q 5");

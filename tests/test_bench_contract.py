@@ -47,7 +47,9 @@ def test_traffic_comes_from_the_committed_profile():
         scaled = k["fetch_size_kib"] * 1024 * prof["calibration"]["fetch_scale"] + \
             k["write_size_kib"] * 1024 * prof["calibration"]["write_scale"]
         assert abs(scaled - k["hbm_bytes"]) <= 2048, key
-        assert 0.99 <= k["hbm_bytes"] / k["algorithmic_bytes"] <= 1.5, key
+        # plausible: at least the algorithmic bytes, at most 2x (the heaviest-first
+        # forward order re-reads the K / V rows of each head's short q tiles)
+        assert 0.99 <= k["hbm_bytes"] / k["algorithmic_bytes"] <= 2.0, key
 
 
 def test_config2_flops_are_the_kept_block_count():

@@ -444,7 +444,7 @@ def test_dkdv_any_cut_of_the_work_list_matches_oracle(chunk, dtype):
         dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), delta.data_ptr(), code, B, H, H_kv, N, N, D,
         L.row_ptr.data_ptr(), L.row_idx.data_ptr(), sched.n_qt, L.col_ptr.data_ptr(),
         L.col_idx.data_ptr(), sched.n_kt, items_d.data_ptr(), len(items), split_d.data_ptr(),
-        len(split), n_pslots, partials.data_ptr(), mask.data_ptr(), n_b, n_b, bm, bm,
+        len(split), n_pslots, partials.data_ptr(), None, mask.data_ptr(), n_b, n_b, bm, bm,
         1.0 / math.sqrt(D), 1, S, W, torch.cuda.current_stream().cuda_stream)
     assert rc == 0, lib.gki_last_error()
     torch.cuda.synchronize()
@@ -582,6 +582,42 @@ def test_fwd_order_entries_out_of_range_do_nothing():
         else:
             assert (o_hole[b, h, rows].view(torch.int16) == 0x7E7E).all(), unit
             assert (l_hole[b, h, rows] == -7.0).all(), unit
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_dq_order_gives_the_index_order_bits(dtype):
+    """gki_bsa_bwd with the schedule's dQ order table (what the op passes) and
+    with none (index order) writes the same dQ, dK, dV bits."""
+    print(f"[case] dQ order {dtype}", flush=True)
+    B, H, N, D, S, W, bm = 2, 4, 1000, 64, 4, 256, 64
+    q, k, v, do = _inputs((B, H, N, D), (B, H, N, D), dtype, seed=29, grad_out=True)
+    mask = stk.make_streaming_mask(N, N, stk.StreamingMaskSpec(S, W), bm, bm, device=DEV)
+    leaves = [t.detach().requires_grad_(True) for t in (q, k, v)]
+    out = stk.block_sparse_attention(*leaves, mask, block_m=bm, block_n=bm, is_causal=True,
+                                     sink_size=S, window_size=W)
+    lse = out.grad_fn.saved_tensors[4]
+    out.backward(do)
+    sched = bwd_schedule(mask, N, N, bm, bm, True, S, W, group=1, bh_kv=B * H)   # the op's own
+    assert sorted(sched.dq_order.cpu().tolist()) == list(range(sched.n_qt * B * H))
+    L = sched.lists
+    partials = torch.empty(max(B * H * sched.n_pslots * 2 * 64 * D, 1), dtype=torch.float32, device=DEV)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    delta = torch.empty((B, H, N), dtype=torch.float32, device=DEV)
+    n_b = (N + bm - 1) // bm
+    lib = _lib.load()
+    rc = lib.gki_bsa_bwd(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), do.data_ptr(), lse.data_ptr(),
+        dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), delta.data_ptr(),
+        {torch.float32: 0, torch.bfloat16: 2}[dtype], B, H, H, N, N, D,
+        L.row_ptr.data_ptr(), L.row_buf.data_ptr(), sched.n_qt, L.col_ptr.data_ptr(),
+        L.col_buf.data_ptr(), sched.n_kt, sched.items.data_ptr(), sched.n_items,
+        sched.split.data_ptr(), sched.n_split, sched.n_pslots, partials.data_ptr(), None,
+        mask.data_ptr(), n_b, n_b, bm, bm, 1.0 / math.sqrt(D), 1, S, W,
+        torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, lib.gki_last_error()
+    torch.cuda.synchronize()
+    for name, got, ref in zip(("dQ", "dK", "dV"), (dq, dk, dv), [t.grad for t in leaves]):
+        assert torch.equal(got, ref), name
 
 
 def test_fwd_bwd_deterministic():

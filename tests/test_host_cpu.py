@@ -104,7 +104,7 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(lib, name), f"{name} declared in gki_bsa.h but not exported"
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
     assert set(_lib.SIGNATURES) == set(names)
-    assert lib.gki_abi_version() == 5
+    assert lib.gki_abi_version() == 6
 
 
 def test_dkdv_work_list_matches_oracle():
