@@ -521,9 +521,9 @@ __host__ __device__ inline int xcd_remap(int b, int n) { return xcd_start(b % kX
 // Wave issue priority around a cluster of MFMAs (ON: the D <= 64 kernels).
 // While a wave issues its products it wins the SIMD's issue arbitration over
 // the waves in their softmax / dS VALU phase, so the matrix pipe is fed more
-// evenly: forward -2%, backward -0.5 to -1.3% at D = 64 (c3, c5); at
-// D = 128 (two waves per SIMD) it made the forward 3% slower, so it is off
-// there.
+// evenly: at D = 64 (four waves per SIMD) the forward ran 2% and the
+// backward 0.5-1.3% faster on long StreamingLLM sequences; at D = 128 (two
+// waves per SIMD) it made the forward 3% slower, so it is off there.
 template <bool ON>
 __device__ inline void mfma_priority_hi() {
   if constexpr (ON) __builtin_amdgcn_s_setprio(1);
