@@ -251,12 +251,12 @@ def section_c4(steps: int, warmup: int, cpu_sample: Optional[dict] = None) -> di
 
     import sparse_triton_kernel as stk
 
+    from benchmark import seeded_normal
+
     B, H, NKV, D, S, W = 8, 32, 100000, 128, 4, 2048
     dev = torch.device("cuda:0")
-    g = torch.Generator(device=dev).manual_seed(3)
-    q = torch.randn(B, H, 1, D, generator=g, device=dev).to(torch.bfloat16)
-    k = torch.randn(B, H, NKV, D, generator=g, device=dev).to(torch.bfloat16)
-    v = torch.randn(B, H, NKV, D, generator=g, device=dev).to(torch.bfloat16)
+    q, k, v = seeded_normal([(B, H, 1, D), (B, H, NKV, D), (B, H, NKV, D)], 3, torch.bfloat16, dev,
+                            workers=cpu_threads())
     mask = stk.make_streaming_mask(1, NKV, stk.StreamingMaskSpec(S, W), 1, 64, device=dev)
     kept = int(mask.sum().item())
     exact_bytes = (S + W) * D * 2 * 2 * B * H
@@ -303,11 +303,11 @@ def _gqa_c4(B, H, NKV, D, S, W, mask, steps, warmup, H_kv=8, n_q=1) -> dict:
 
     import sparse_triton_kernel as stk
 
+    from benchmark import seeded_normal
+
     dev = torch.device("cuda:0")
-    g = torch.Generator(device=dev).manual_seed(5)
-    q = torch.randn(B, H, n_q, D, generator=g, device=dev).to(torch.bfloat16)
-    k = torch.randn(B, H_kv, NKV, D, generator=g, device=dev).to(torch.bfloat16)
-    v = torch.randn(B, H_kv, NKV, D, generator=g, device=dev).to(torch.bfloat16)
+    q, k, v = seeded_normal([(B, H, n_q, D), (B, H_kv, NKV, D), (B, H_kv, NKV, D)], 5, torch.bfloat16,
+                            dev, workers=cpu_threads())
     if n_q != 1:
         mask = stk.make_streaming_mask(n_q, NKV, stk.StreamingMaskSpec(S, W), 1, 64, device=dev)
 
@@ -362,10 +362,11 @@ def section_c5(steps: int, warmup: int) -> dict:
 
     import sparse_triton_kernel as stk
 
+    from benchmark import seeded_normal
+
     B, H, N, D, S, W, bm, bn = 1, 16, 131072, 64, 4, 4096, 128, 64
     dev = torch.device("cuda:0")
-    g = torch.Generator(device=dev).manual_seed(4)
-    q, k, v, do = (torch.randn(B, H, N, D, generator=g, device=dev).to(torch.bfloat16) for _ in range(4))
+    q, k, v, do = seeded_normal([(B, H, N, D)] * 4, 4, torch.bfloat16, dev, workers=cpu_threads())
     q, k, v = (t.requires_grad_(True) for t in (q, k, v))
     mask = stk.make_streaming_mask(N, N, stk.StreamingMaskSpec(S, W), bm, bn, device=dev)
     kept = int(mask.sum().item())

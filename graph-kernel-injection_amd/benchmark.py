@@ -24,11 +24,14 @@ Usage (from ``graph-kernel-injection_amd/``)::
 from __future__ import annotations
 
 import argparse
+import concurrent.futures as cf
 import csv
 import dataclasses
+import hashlib
 import math
 import statistics
 import sys
+import threading
 import time
 from dataclasses import dataclass
 from pathlib import Path
@@ -107,6 +110,50 @@ def percentile(values: Sequence[float], q: float) -> float:
     k = (len(s) - 1) * (q / 100.0)
     lo, hi = math.floor(k), math.ceil(k)
     return s[lo] if lo == hi else s[lo] + (s[hi] - s[lo]) * (k - lo)
+
+
+# Elements per chunk of seeded_normal: each chunk has its own CPU generator.
+SEED_CHUNK = 1 << 24
+
+
+def _chunk_seed(seed: int, tensor: int, chunk: int) -> int:
+    return int.from_bytes(hashlib.blake2b(f"{seed}/{tensor}/{chunk}".encode(), digest_size=8).digest(),
+                          "little") >> 1
+
+
+def seeded_normal(shapes: Sequence[Sequence[int]], seed: int, dtype: torch.dtype,
+                  device, scale: float = 1.0, workers: int = 16) -> List[torch.Tensor]:
+    """Tensors of N(0, scale^2) values (drawn in fp32, scaled, then rounded to
+    ``dtype``) generated on the CPU and moved to ``device``: the same bits on
+    every host and GPU, as a CPU ``torch.Generator`` seeded per config gives
+    (the protocol of SURVEY's measurement plan; the reference draws q, k, v in
+    order from one generator, benchmark.py:128-133). Tensor t's elements come
+    in chunks of SEED_CHUNK, chunk c from a generator seeded by a hash of
+    (seed, t, c), so the draw of a decode step's 6.5e9 K / V values runs on
+    ``workers`` threads instead of one generator's ~40 s."""
+    flats = [torch.empty(math.prod(s), dtype=dtype) for s in shapes]
+    jobs = [(t, a) for t, f in enumerate(flats) for a in range(0, f.numel(), SEED_CHUNK)]
+    local = threading.local()
+
+    def draw(job):
+        t, a = job
+        n = min(SEED_CHUNK, flats[t].numel() - a)
+        if not hasattr(local, "buf"):     # one fp32 chunk buffer per thread
+            local.buf = torch.empty(SEED_CHUNK, dtype=torch.float32)
+        g = torch.Generator().manual_seed(_chunk_seed(seed, t, a // SEED_CHUNK))
+        x = torch.randn(n, generator=g, dtype=torch.float32, out=local.buf[:n])
+        if scale != 1.0:
+            x.mul_(scale)
+        flats[t][a:a + n].copy_(x)
+
+    intra = torch.get_num_threads()
+    torch.set_num_threads(1)     # one thread per chunk; no nested intra-op pools
+    try:
+        with cf.ThreadPoolExecutor(max_workers=max(1, workers)) as pool:
+            list(pool.map(draw, jobs))
+    finally:
+        torch.set_num_threads(intra)
+    return [f.view(*s).to(device) for f, s in zip(flats, shapes)]
 
 
 def _make_qkv(cfg: HarnessConfig, dtype: torch.dtype, requires_grad: bool = False):

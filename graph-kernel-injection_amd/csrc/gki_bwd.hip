@@ -5,12 +5,17 @@
 //   * `_bwd_preprocess_kernel` (sparse_triton_kernel.py:354-392),
 //       Delta[q] = sum_d fp32(O) * fp32(dO) over the stored O: for 16-bit
 //       inputs inside dq_kernel_16, which runs first and stores -Delta for
-//       dK/dV; for fp32 inputs delta_kernel, before the other two.
+//       dK/dV; for fp32 inputs delta_kernel, before the other two. For 16-bit
+//       inputs the dQ kernel also turns the stored natural LSE into base 2
+//       once per row (second half of the row-term workspace), so the 16-bit
+//       kernels form P = exp(S scale - LSE) as one exp2 of an fma; the fp32
+//       kernels form it as exp2(fma(S, scale, -LSE) log2 e) from the stored
+//       LSE, as the fp32 forward computed its exponents.
 //   * dkdv_kernel   <- `_bwd_dkdv_kernel` (sparse_triton_kernel.py:394-509):
 //       one workgroup per 64-row KV tile, loop over the kept q tiles of its
-//       column (CSC list), P = exp(S - LSE) (as exp2 of base-2 terms; the
-//       forward stores the LSE in base 2), dV += P^T dO, dS = P (dP - Delta)
-//       * scale, dK += dS^T Q. No atomics; one store per tile.
+//       column (CSC list), P = exp(S - LSE), dV += P^T dO,
+//       dS = P (dP - Delta) * scale, dK += dS^T Q. No atomics; one store per
+//       tile.
 //   * dq_kernel     <- `_bwd_dq_kernel` (sparse_triton_kernel.py:511-601):
 //       one workgroup per 64-row q tile, loop over its kept kv tiles (CSR),
 //       dQ += dS K.
@@ -175,16 +180,19 @@ __global__ __launch_bounds__(256) void dkdv_reduce_kernel(Geom g, KvWork w,
 // dK / dV, 16-bit. Q and dO tiles row-major in LDS (double-buffered, staged by
 // LDS-DMA); the dV += P^T dO and dK += dS^T Q operands dO / Q come from lds_tr8.
 // ---------------------------------------------------------------------------
-// DEFER (Geom::defer_scale): dS is cast as P (dP - Delta) and the scale is
-// applied to the fp32 dK / dQ sums (a power-of-two scale on bf16 inputs, the
-// same products); otherwise dS = P (dP - Delta) scale before the cast, as the
-// reference. A template parameter, so neither form carries a branch.
-template <typename T, int D, bool DEFER>
+// PRE (Geom::prescale): the scale is already inside the dP accumulator
+// (V / dO operands and Delta pre-multiplied by a power-of-two scale, exact),
+// so dS = P * acc; otherwise dS = P * (acc * scale). Either way the scaled dS
+// is cast, as the reference. A template parameter, so neither form carries a
+// branch.
+template <typename T, int D, bool PRE>
 __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
     Geom g, const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const uint16_t* __restrict__ V, const uint16_t* __restrict__ dO, uint16_t* __restrict__ dK,
-    uint16_t* __restrict__ dV, const float* __restrict__ LSE, const float* __restrict__ Delta,
+    uint16_t* __restrict__ dV, const float* __restrict__ LSE2, const float* __restrict__ Delta,
     const int32_t* __restrict__ col_ptr, const int32_t* __restrict__ col_idx, KvWork w) {
+  // LSE2: base-2 LSE rows; Delta: -Delta rows (times the scale when PRE),
+  // both written by the dQ kernel, which runs first
   constexpr int KS = (D + 31) / 32;
   constexpr int DT = D / 16;
   using Tile = RowTile<D>;
@@ -213,6 +221,7 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
     const bool ok = my_kv < g.n_kv && d0 < D;
     kf[ks] = ok ? *(const uint4*)(K + kb + (size_t)my_kv * D + d0) : make_uint4(0, 0, 0, 0);
     vf[ks] = ok ? *(const uint4*)(V + kb + (size_t)my_kv * D + d0) : make_uint4(0, 0, 0, 0);
+    if constexpr (PRE) vf[ks] = scale8<T>(vf[ks], g.scale);
   }
   floatx4 dk[DT], dv[DT];
 #pragma unroll
@@ -240,7 +249,7 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
       dma_wait();   // nothing of this branch pending where it rejoins the DMA path
     }
     if (wave_u < 2) {
-      const float* src = (wave_u == 0 ? LSE : Delta) + (size_t)bhq * g.n_q + min(q0 + lane, g.n_q - 1);
+      const float* src = (wave_u == 0 ? LSE2 : Delta) + (size_t)bhq * g.n_q + min(q0 + lane, g.n_q - 1);
       dma_load4(src, lds_addr(wave_u == 0 ? slse[buf] : sdlt[buf]));
     }
   };
@@ -276,7 +285,7 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       // the dP accumulator starts at -Delta of its four q rows (stored negated
-      // by the dQ kernel), so it ends as dP - Delta: dS = P * acc * scale
+      // by the dQ kernel), so it ends as dP - Delta (times the scale when PRE)
       const int qr0 = rho(t, 4 * grp);
       const float4 lse4 = *(const float4*)(&slse[buf][qr0]);
       const float4 ndl4 = *(const float4*)(&sdlt[buf][qr0]);
@@ -298,7 +307,7 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
       for (int i = 0; i < 4; ++i) {
         const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], g.scale_log2, -lv[i]));
         p[t][i] = pv;
-        ds[t][i] = DEFER ? pv * dp[i] : pv * (dp[i] * g.scale);
+        ds[t][i] = PRE ? pv * dp[i] : pv * (dp[i] * g.scale);
       }
     }
     // Masked elements: P = dS = 0 (a bit select, so an exp that overflowed on
@@ -331,10 +340,6 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
   }
 
   // dK/dV accumulators: lane holds rows k_w + 4grp + i, column 16dt + col.
-  if constexpr (DEFER) {
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) dk[dt] *= g.scale;
-  }
   if (item.pslot >= 0) {             // a split column: fp32 partials for the reduce
     float* pk = w.partials + ((size_t)bh * w.n_pslots + item.pslot) * 2 * (kTileN * D);
     float* pv = pk + kTileN * D;
@@ -363,13 +368,241 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
 }
 
 // ---------------------------------------------------------------------------
+// dK / dV, 16-bit, head_dim 64, in quadrants: wave w owns kv rows
+// 32 (w & 1) .. +31 of the 64-row kv tile (two 16-row blocks, K / V in
+// registers as the B operands) against q rows 32 (w >> 1) .. +31 of each q
+// tile (rho subtiles 2 qh, 2 qh + 1). Every Q / dO row read, LSE / Delta read
+// and transposed Q / dO read from LDS then feeds the MFMAs of both kv blocks:
+// 28 LDS reads per 32 MFMAs per wave and tile instead of 56. The two q
+// halves' fp32 dK / dV sums meet once, through LDS, at the end of the item
+// (the qh = 0 wave adds the qh = 1 wave's, a fixed order).
+// ---------------------------------------------------------------------------
+template <typename T, bool PRE>
+__global__ __launch_bounds__(256, 3) void dkdv_kernel_q64(
+    Geom g, const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+    const uint16_t* __restrict__ V, const uint16_t* __restrict__ dO, uint16_t* __restrict__ dK,
+    uint16_t* __restrict__ dV, const float* __restrict__ LSE2, const float* __restrict__ Delta,
+    const int32_t* __restrict__ col_ptr, const int32_t* __restrict__ col_idx, KvWork w) {
+  // LSE2: base-2 LSE rows; Delta: -Delta rows (times the scale when PRE),
+  // both written by the dQ kernel, which runs first
+  constexpr int D = 64, KS = 2, DT = 4;
+  using Tile = RowTile<D>;
+  __shared__ __align__(16) uint16_t sq[2][64 * D];
+  __shared__ __align__(16) uint16_t sdo[2][64 * D];
+  __shared__ __align__(16) float slse[2][64];
+  __shared__ __align__(16) float sdlt[2][64];
+
+  const int BH = g.B * g.H_kv;
+  int bh;
+  const KvItem item = kv_item_of(blockIdx.x, BH, w, bh);
+  const int kt = item.kt;
+  const size_t kb = (size_t)bh * g.n_kv * D;
+  const int bhq0 = (bh / g.H_kv) * g.H + (bh % g.H_kv) * g.group;   // first q head
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int grp = lane >> 4, col = lane & 15;
+  const int kh = __builtin_amdgcn_readfirstlane(wave & 1), qh = __builtin_amdgcn_readfirstlane(wave >> 1);
+  const int k_w = kt * kTileN + 32 * kh;       // the wave's first kv row
+
+  uint4 kf[2][KS], vf[2][KS];
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    const int my_kv = k_w + 16 * b + col;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int d0 = 32 * ks + 8 * grp;
+      const bool ok = my_kv < g.n_kv;
+      kf[b][ks] = ok ? *(const uint4*)(K + kb + (size_t)my_kv * D + d0) : make_uint4(0, 0, 0, 0);
+      vf[b][ks] = ok ? *(const uint4*)(V + kb + (size_t)my_kv * D + d0) : make_uint4(0, 0, 0, 0);
+      if constexpr (PRE) vf[b][ks] = scale8<T>(vf[b][ks], g.scale);
+    }
+  }
+  floatx4 dk[2][DT], dv[2][DT];
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int i = 0; i < DT; ++i) dk[b][i] = dv[b][i] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  const int e_beg = col_ptr[kt], e_end = col_ptr[kt + 1];
+  DmaTile<D> dma;
+  dma.init(tid);
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  auto load_tile = [&](int q0, int bhq, int buf) {
+    const size_t qb = (size_t)bhq * g.n_q * D;
+    if (q0 + kTileM <= g.n_q) {
+      dma.load(Q + qb, q0, sq[buf]);
+      dma.load(dO + qb, q0, sdo[buf]);
+    } else {
+      Tile t;
+      t.load(Q + qb, q0, g.n_q, tid);
+      t.store(sq[buf], tid);
+      t.load(dO + qb, q0, g.n_q, tid);
+      t.store(sdo[buf], tid);
+      dma_wait();   // nothing of this branch pending where it rejoins the DMA path
+    }
+    if (wave_u < 2) {
+      const float* src = (wave_u == 0 ? LSE2 : Delta) + (size_t)bhq * g.n_q + min(q0 + lane, g.n_q - 1);
+      dma_load4(src, lds_addr(wave_u == 0 ? slse[buf] : sdlt[buf]));
+    }
+  };
+  const int L = e_end - e_beg;
+  const int n_it = item.it1 - item.it0;
+  const int h0 = L > 0 ? item.it0 / L : 0;
+  int e_nx = e_beg + (item.it0 - h0 * L), q_nx = bhq0 + h0;
+  if (n_it > 0) load_tile((col_idx[e_nx] & kIdxMask) * kTileM, q_nx, 0);
+  dma_wait();
+  __syncthreads();
+
+  const int kv_hi_wave = min(k_w + 31, g.n_kv - 1);
+  for (int it = 0; it < n_it; ++it) {
+    const int buf = it & 1;
+    const int ent = col_idx[e_nx];
+    if (++e_nx == e_end) {
+      e_nx = e_beg;
+      ++q_nx;
+    }
+    const int q0 = (ent & kIdxMask) * kTileM;
+    const bool partial = (ent >> kPartialBit) & 1;
+    if (it + 1 < n_it) load_tile((col_idx[e_nx] & kIdxMask) * kTileM, q_nx, buf ^ 1);
+    const uint16_t* cq = sq[buf];
+    const uint16_t* cdo = sdo[buf];
+    const int qw0 = q0 + 32 * qh;              // the wave's first q row
+    const bool need_mask = partial || (qw0 + 32 > g.n_q) || (k_w + 31 >= g.n_kv) ||
+                           !tile_all_visible(g, qw0, min(qw0 + 31, g.n_q - 1), k_w, kv_hi_wave);
+    floatx4 p[2][2], ds[2][2];                 // [subtile 2 qh + u][kv block]
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int t = 2 * qh + u;
+      const int qr0 = rho(t, 4 * grp);
+      const float4 lse4 = *(const float4*)(&slse[buf][qr0]);
+      const float4 ndl4 = *(const float4*)(&sdlt[buf][qr0]);
+      floatx4 sc[2], dp[2];
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        sc[b] = floatx4{0.f, 0.f, 0.f, 0.f};
+        dp[b] = floatx4{ndl4.x, ndl4.y, ndl4.z, ndl4.w};
+      }
+      const int r = rho(t, col);
+      mfma_priority_hi<true>();
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int d0 = 32 * ks + 8 * grp;
+        const uint4 aq = lds_row8<D>(cq, r, d0);
+        const uint4 ad = lds_row8<D>(cdo, r, d0);
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+          sc[b] = T::mfma(aq, kf[b][ks], sc[b]);
+          dp[b] = T::mfma(ad, vf[b][ks], dp[b]);
+        }
+      }
+      mfma_priority_lo<true>();
+      const float lv[4] = {lse4.x, lse4.y, lse4.z, lse4.w};
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[b][i], g.scale_log2, -lv[i]));
+          p[u][b][i] = pv;
+          ds[u][b][i] = PRE ? pv * dp[b][i] : pv * (dp[b][i] * g.scale);
+        }
+    }
+    if (need_mask) {     // masked elements: P = dS = 0 (bit select)
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        const LaneBits vis(col_valid_bits(g, k_w + 16 * b + col, q0, partial), grp);
+        const uint32_t wq = qh ? vis.w[1] : vis.w[0];   // uniform select, not an index
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int m = __builtin_amdgcn_sbfe((int)wq, 4 * u + i, 1);   // 0 or -1
+            p[u][b][i] = __int_as_float(__float_as_int(p[u][b][i]) & m);
+            ds[u][b][i] = __int_as_float(__float_as_int(ds[u][b][i]) & m);
+          }
+      }
+    }
+    uint4 ap[2], as[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      ap[b] = pack8<T>(p[0][b], p[1][b]);
+      as[b] = pack8<T>(ds[0][b], ds[1][b]);
+    }
+    mfma_priority_hi<true>();
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const uint4 bo = lds_tr8<D>(cdo, 32 * qh, 16 * dt, lane);
+      const uint4 bq = lds_tr8<D>(cq, 32 * qh, 16 * dt, lane);
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        dv[b][dt] = T::mfma(ap[b], bo, dv[b][dt]);
+        dk[b][dt] = T::mfma(as[b], bq, dk[b][dt]);
+      }
+    }
+    mfma_priority_lo<true>();
+    dma_wait();        // the next tile's LDS-DMA has landed before the barrier
+    __syncthreads();
+  }
+
+  // the q-half sums meet in LDS (the Q / dO buffers are free: every wave passed
+  // the loop's last barrier): qh = 1 waves store, qh = 0 waves add theirs first
+  floatx4* red = (floatx4*)&sq[0][0] + kh * (4 * DT * 64);
+  if (qh == 1) {
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        red[((2 * b + 0) * DT + dt) * 64 + lane] = dk[b][dt];
+        red[((2 * b + 1) * DT + dt) * 64 + lane] = dv[b][dt];
+      }
+  }
+  __syncthreads();
+  if (qh == 1) return;
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      dk[b][dt] += red[((2 * b + 0) * DT + dt) * 64 + lane];
+      dv[b][dt] += red[((2 * b + 1) * DT + dt) * 64 + lane];
+    }
+  // accumulators: lane holds kv rows k_w + 16 b + 4 grp + i, column 16 dt + col
+  if (item.pslot >= 0) {             // a split column: fp32 partials for the reduce
+    float* pk = w.partials + ((size_t)bh * w.n_pslots + item.pslot) * 2 * (kTileN * D);
+    float* pv = pk + kTileN * D;
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 32 * kh + 16 * b + 4 * grp + i;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          pk[r * D + 16 * dt + col] = dk[b][dt][i];
+          pv[r * D + 16 * dt + col] = dv[b][dt][i];
+        }
+      }
+    return;
+  }
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = k_w + 16 * b + 4 * grp + i;
+      if (row < g.n_kv) {
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          dK[kb + (size_t)row * D + 16 * dt + col] = T::from_float(dk[b][dt][i]);
+          dV[kb + (size_t)row * D + 16 * dt + col] = T::from_float(dv[b][dt][i]);
+        }
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // dK / dV, fp32
 // ---------------------------------------------------------------------------
 template <int D>
 struct DkdvSmem32 {
   float q[64 * (D + 4)];
   float dout[64 * (D + 4)];
-  float lse2[64];
+  float lse[64];
   float dlt[64];
 };
 
@@ -379,6 +612,7 @@ __global__ __launch_bounds__(256, D >= 128 ? 1 : 2) void dkdv_kernel_32(
     const float* __restrict__ dO, float* __restrict__ dK, float* __restrict__ dV,
     const float* __restrict__ LSE, const float* __restrict__ Delta,
     const int32_t* __restrict__ col_ptr, const int32_t* __restrict__ col_idx, KvWork w) {
+  // LSE: the forward's natural LSE; Delta: rowsum(O dO) from delta_kernel
   constexpr int KS = D / 4;
   constexpr int DT = D / 16;
   constexpr int LD = D + 4;
@@ -416,7 +650,7 @@ __global__ __launch_bounds__(256, D >= 128 ? 1 : 2) void dkdv_kernel_32(
     sdo.load(dO + qb, q0, g.n_q, tid);
     if (tid < 64) {
       const int r = q0 + tid;
-      lreg = r < g.n_q ? LSE[(size_t)bhq * g.n_q + r] : 0.f;   // base 2
+      lreg = r < g.n_q ? LSE[(size_t)bhq * g.n_q + r] : 0.f;
       dreg = r < g.n_q ? Delta[(size_t)bhq * g.n_q + r] : 0.f;
     }
   };
@@ -439,7 +673,7 @@ __global__ __launch_bounds__(256, D >= 128 ? 1 : 2) void dkdv_kernel_32(
     sq.store(sm.q, tid);
     sdo.store(sm.dout, tid);
     if (tid < 64) {
-      sm.lse2[tid] = lreg;
+      sm.lse[tid] = lreg;
       sm.dlt[tid] = dreg;
     }
     __syncthreads();
@@ -447,11 +681,11 @@ __global__ __launch_bounds__(256, D >= 128 ? 1 : 2) void dkdv_kernel_32(
 
     const bool need_mask = partial || (q0 + kTileM > g.n_q) || (k_w + 15 >= g.n_kv) ||
                            !tile_all_visible(g, q0, min(q0 + kTileM - 1, g.n_q - 1), k_w, kv_hi_wave);
-    floatx4 fk[DT], fv[DT];            // this iteration's 64 rows
-#pragma unroll
-    for (int i = 0; i < DT; ++i) fk[i] = fv[i] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
+      floatx4 fk[DT], fv[DT];          // this subtile's 16 rows, folded in compensated
+#pragma unroll
+      for (int i = 0; i < DT; ++i) fk[i] = fv[i] = floatx4{0.f, 0.f, 0.f, 0.f};
       const int r = rho(t, col);
       const floatx4 s = mfma_f32_dot<KS>([&](int ks) { return sm.q[r * LD + 4 * ks + grp]; },
                                          [&](int ks) { return kf[ks]; });
@@ -460,7 +694,7 @@ __global__ __launch_bounds__(256, D >= 128 ? 1 : 2) void dkdv_kernel_32(
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int qr = rho(t, 4 * grp + i);
-        float pv = __builtin_amdgcn_exp2f(s[i] * g.scale_log2 - sm.lse2[qr]);
+        float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], g.scale, -sm.lse[qr]) * kLog2e);
         if (need_mask && !elem_valid(g, q0 + qr, my_kv, partial)) pv = 0.f;
         const float dsv = pv * (dp[i] - sm.dlt[qr]) * g.scale;
 #pragma unroll
@@ -469,11 +703,11 @@ __global__ __launch_bounds__(256, D >= 128 ? 1 : 2) void dkdv_kernel_32(
           fk[dt] = mfma_f32(dsv, sm.q[qr * LD + 16 * dt + col], fk[dt]);
         }
       }
-    }
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      two_sum_fold(dk[dt], ck[dt], fk[dt]);
-      two_sum_fold(dv[dt], cv[dt], fv[dt]);
+      for (int dt = 0; dt < DT; ++dt) {
+        two_sum_fold(dk[dt], ck[dt], fk[dt]);
+        two_sum_fold(dv[dt], cv[dt], fv[dt]);
+      }
     }
   }
 #pragma unroll
@@ -513,7 +747,7 @@ __global__ __launch_bounds__(256, D >= 128 ? 1 : 2) void dkdv_kernel_32(
 // LDS-DMA); the
 // dQ^T += K^T dS^T operand K^T comes from lds_tr8.
 // ---------------------------------------------------------------------------
-template <typename T, int D, bool DEFER>
+template <typename T, int D, bool PRE>
 __global__ __launch_bounds__(256, 2) void dq_kernel_16(
     Geom g, const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const uint16_t* __restrict__ V, const uint16_t* __restrict__ O, const uint16_t* __restrict__ dO,
@@ -545,12 +779,13 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_16(
     qf[ks] = ok ? *(const uint4*)(Q + qb + (size_t)my_q * D + d0) : make_uint4(0, 0, 0, 0);
     df[ks] = ok ? *(const uint4*)(dO + qb + (size_t)my_q * D + d0) : make_uint4(0, 0, 0, 0);
   }
-  const float lse2 = my_q < g.n_q ? LSE[(size_t)bh * g.n_q + my_q] : 0.f;   // base 2
+  // the stored natural LSE in base 2 (one rounding, once per row)
+  const float lse2 = my_q < g.n_q ? lse_base2(LSE[(size_t)bh * g.n_q + my_q]) : 0.f;
   // Delta = rowsum(O * dO) in fp32 over the stored O (the preprocessing pass,
   // sparse_triton_kernel.py:354-392, fused here): the lane already holds its
   // row's dO chunks, the four lane groups of a row are summed across. Every q
-  // row has exactly one dQ workgroup, which writes it for the dK/dV kernel
-  // that runs next.
+  // row has exactly one dQ workgroup, which writes it (and the base-2 LSE)
+  // for the dK/dV kernel that runs next.
   float part = 0.f;
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
@@ -564,9 +799,17 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_16(
     }
   }
   // Stored negated: both kernels start their dP accumulators at -Delta, so
-  // they end as dP - Delta (the scale: see DEFER).
-  const float ndlt = -wave_sum16x4(part);
-  if (my_q < g.n_q && grp == 0) Delta[(size_t)bh * g.n_q + my_q] = ndlt;
+  // they end as dP - Delta. With PRE the dO operand and -Delta carry the
+  // (power-of-two) scale, so the accumulators end as (dP - Delta) * scale.
+  const float ndlt = PRE ? -wave_sum16x4(part) * g.scale : -wave_sum16x4(part);
+  if constexpr (PRE) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) df[ks] = scale8<T>(df[ks], g.scale);
+  }
+  if (my_q < g.n_q && grp == 0) {
+    Delta[(size_t)bh * g.n_q + my_q] = ndlt;
+    Delta[(size_t)g.B * g.H * g.n_q + (size_t)bh * g.n_q + my_q] = lse2;
+  }
 
   floatx4 dq[DT];
 #pragma unroll
@@ -624,7 +867,7 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_16(
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], g.scale_log2, -lse2));
-        ds[t][i] = DEFER ? pv * dp[i] : pv * (dp[i] * g.scale);
+        ds[t][i] = PRE ? pv * dp[i] : pv * (dp[i] * g.scale);
       }
     }
     if (need_mask) {     // masked elements: dS = 0 (bit select, as in the dK/dV kernel)
@@ -649,9 +892,198 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_16(
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
       uint2 w;
-      const float sc = DEFER ? g.scale : 1.f;
-      w.x = pack2<T>(dq[dt][0] * sc, dq[dt][1] * sc);
-      w.y = pack2<T>(dq[dt][2] * sc, dq[dt][3] * sc);
+      w.x = pack2<T>(dq[dt][0], dq[dt][1]);
+      w.y = pack2<T>(dq[dt][2], dq[dt][3]);
+      *(uint2*)(dQ + qb + (size_t)my_q * D + 16 * dt + 4 * grp) = w;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dQ, 16-bit, head_dim 64, in quadrants: wave w owns q rows 32 (w >> 1) ..
+// +31 of the 64-row q tile (two 16-row blocks, the MFMAs' B-operand columns)
+// against kv rows 32 (w & 1) .. +31 of each kv tile (rho subtiles 2 kh,
+// 2 kh + 1). Every K / V row read and every K^T transposed read from LDS then
+// feeds the MFMAs of both q blocks: 16 LDS reads per 24 MFMAs per wave and
+// tile instead of 32. The two kv halves' fp32 dQ sums meet once, through LDS,
+// at the end (the kh = 0 wave adds the kh = 1 wave's, a fixed order).
+// ---------------------------------------------------------------------------
+template <typename T, bool PRE>
+__global__ __launch_bounds__(256, 4) void dq_kernel_q64(
+    Geom g, const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+    const uint16_t* __restrict__ V, const uint16_t* __restrict__ O, const uint16_t* __restrict__ dO,
+    uint16_t* __restrict__ dQ, const float* __restrict__ LSE, float* __restrict__ Delta,
+    const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ row_idx, int n_qt,
+    const int32_t* __restrict__ dq_order) {
+  constexpr int D = 64, KS = 2, DT = 4;
+  using Tile = RowTile<D>;
+  __shared__ __align__(16) uint16_t sk[2][64 * D];
+  __shared__ __align__(16) uint16_t sv[2][64 * D];
+
+  const int n_wg = n_qt * g.B * g.H;
+  const int wg = work_of(blockIdx.x, n_wg, dq_order);
+  if (wg < 0) return;
+  const int bh = wg / n_qt, qt = wg - bh * n_qt;
+  const size_t qb = (size_t)bh * g.n_q * D;
+  const size_t kb = (size_t)kv_bh(g, bh) * g.n_kv * D;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int grp = lane >> 4, col = lane & 15;
+  const int qh = __builtin_amdgcn_readfirstlane(wave >> 1), kh = __builtin_amdgcn_readfirstlane(wave & 1);
+  const int q0w = qt * kTileM + 32 * qh;       // the wave's first q row
+
+  uint4 qf[2][KS], df[2][KS];
+  float lse2[2], ndlt[2];
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    const int my_q = q0w + 16 * b + col;
+    const bool ok = my_q < g.n_q;
+    float part = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int d0 = 32 * ks + 8 * grp;
+      qf[b][ks] = ok ? *(const uint4*)(Q + qb + (size_t)my_q * D + d0) : make_uint4(0, 0, 0, 0);
+      df[b][ks] = ok ? *(const uint4*)(dO + qb + (size_t)my_q * D + d0) : make_uint4(0, 0, 0, 0);
+      // Delta = rowsum(O * dO) over the stored O (sparse_triton_kernel.py:354-392)
+      if (ok) {
+        const uint4 o4 = *(const uint4*)(O + qb + (size_t)my_q * D + d0);
+        const uint16_t* ho = (const uint16_t*)&o4;
+        const uint16_t* hd = (const uint16_t*)&df[b][ks];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) part += T::to_float(ho[i]) * T::to_float(hd[i]);
+      }
+    }
+    lse2[b] = ok ? lse_base2(LSE[(size_t)bh * g.n_q + my_q]) : 0.f;
+    // stored negated (and scaled with PRE), as in dq_kernel_16
+    ndlt[b] = PRE ? -wave_sum16x4(part) * g.scale : -wave_sum16x4(part);
+    if constexpr (PRE) {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) df[b][ks] = scale8<T>(df[b][ks], g.scale);
+    }
+    if (ok && grp == 0 && kh == 0) {     // the two kv-half waves hold the same rows
+      Delta[(size_t)bh * g.n_q + my_q] = ndlt[b];
+      Delta[(size_t)g.B * g.H * g.n_q + (size_t)bh * g.n_q + my_q] = lse2[b];
+    }
+  }
+
+  floatx4 dq[2][DT];
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int i = 0; i < DT; ++i) dq[b][i] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  const int e_beg = row_ptr[qt], e_end = row_ptr[qt + 1];
+  DmaTile<D> dma;
+  dma.init(tid);
+  auto stage = [&](int k0, int buf) {
+    if (k0 + kTileN <= g.n_kv) {
+      dma.load(K + kb, k0, sk[buf]);
+      dma.load(V + kb, k0, sv[buf]);
+    } else {
+      Tile t;
+      t.load(K + kb, k0, g.n_kv, tid);
+      t.store(sk[buf], tid);
+      t.load(V + kb, k0, g.n_kv, tid);
+      t.store(sv[buf], tid);
+      dma_wait();   // nothing of this branch pending where it rejoins the DMA path
+    }
+  };
+  if (e_beg < e_end) stage((row_idx[e_beg] & kIdxMask) * kTileN, 0);
+  dma_wait();
+  __syncthreads();
+  const int q_hi_wave = min(q0w + 31, g.n_q - 1);
+  for (int e = e_beg; e < e_end; ++e) {
+    const int buf = (e - e_beg) & 1;
+    const int ent = row_idx[e];
+    const int k0 = (ent & kIdxMask) * kTileN;
+    const bool partial = (ent >> kPartialBit) & 1;
+    if (e + 1 < e_end) stage((row_idx[e + 1] & kIdxMask) * kTileN, buf ^ 1);
+    const uint16_t* ck = sk[buf];
+    const uint16_t* cv = sv[buf];
+    const int kw0 = k0 + 32 * kh;              // the wave's first kv row
+    const bool need_mask = partial || (q0w + 31 >= g.n_q) || (kw0 + 32 > g.n_kv) ||
+                           !tile_all_visible(g, q0w, q_hi_wave, kw0, kw0 + 31);
+    floatx4 ds[2][2];                          // [subtile 2 kh + u][q block]
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int r = rho(2 * kh + u, col);
+      floatx4 sc[2], dp[2];
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        sc[b] = floatx4{0.f, 0.f, 0.f, 0.f};
+        dp[b] = floatx4{ndlt[b], ndlt[b], ndlt[b], ndlt[b]};
+      }
+      mfma_priority_hi<true>();
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int d0 = 32 * ks + 8 * grp;
+        const uint4 ak = lds_row8<D>(ck, r, d0);
+        const uint4 av = lds_row8<D>(cv, r, d0);
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+          sc[b] = T::mfma(ak, qf[b][ks], sc[b]);
+          dp[b] = T::mfma(av, df[b][ks], dp[b]);
+        }
+      }
+      mfma_priority_lo<true>();
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[b][i], g.scale_log2, -lse2[b]));
+          ds[u][b][i] = PRE ? pv * dp[b][i] : pv * (dp[b][i] * g.scale);
+        }
+    }
+    if (need_mask) {     // masked elements: dS = 0 (bit select)
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        const LaneBits vis(row_valid_bits(g, q0w + 16 * b + col, k0, partial), grp);
+        // the word of subtiles 2 kh, 2 kh + 1, chosen by a uniform select (an
+        // index by kh would put the pair in scratch)
+        const uint32_t wk = kh ? vis.w[1] : vis.w[0];
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int m = __builtin_amdgcn_sbfe((int)wk, 4 * u + i, 1);   // 0 or -1
+            ds[u][b][i] = __int_as_float(__float_as_int(ds[u][b][i]) & m);
+          }
+      }
+    }
+    uint4 pb[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) pb[b] = pack8<T>(ds[0][b], ds[1][b]);
+    mfma_priority_hi<true>();
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const uint4 a = lds_tr8<D>(ck, 32 * kh, 16 * dt, lane);
+#pragma unroll
+      for (int b = 0; b < 2; ++b) dq[b][dt] = T::mfma(a, pb[b], dq[b][dt]);
+    }
+    mfma_priority_lo<true>();
+    dma_wait();        // the next tile's LDS-DMA has landed before the barrier
+    __syncthreads();
+  }
+  // the kv-half sums meet in LDS (the K buffers are free: every wave passed the
+  // loop's last barrier): kh = 1 waves store, kh = 0 waves add theirs first
+  floatx4* red = (floatx4*)&sk[0][0] + qh * (2 * DT * 64);
+  if (kh == 1) {
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) red[(b * DT + dt) * 64 + lane] = dq[b][dt];
+  }
+  __syncthreads();
+  if (kh == 1) return;
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    const int my_q = q0w + 16 * b + col;
+    if (my_q >= g.n_q) continue;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const floatx4 o = red[(b * DT + dt) * 64 + lane];
+      uint2 w;
+      w.x = pack2<T>(dq[b][dt][0] + o[0], dq[b][dt][1] + o[1]);
+      w.y = pack2<T>(dq[b][dt][2] + o[2], dq[b][dt][3] + o[3]);
       *(uint2*)(dQ + qb + (size_t)my_q * D + 16 * dt + 4 * grp) = w;
     }
   }
@@ -696,7 +1128,7 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_32(
     qf[ks] = ok ? Q[qb + (size_t)my_q * D + 4 * ks + grp] : 0.f;
     df[ks] = ok ? dO[qb + (size_t)my_q * D + 4 * ks + grp] : 0.f;
   }
-  const float lse2 = my_q < g.n_q ? LSE[(size_t)bh * g.n_q + my_q] : 0.f;   // base 2
+  const float lse = my_q < g.n_q ? LSE[(size_t)bh * g.n_q + my_q] : 0.f;   // natural
   const float dlt = my_q < g.n_q ? Delta[(size_t)bh * g.n_q + my_q] : 0.f;
   floatx4 dq[DT], cq[DT];              // running sum and its compensation (two_sum_fold)
 #pragma unroll
@@ -724,11 +1156,11 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_32(
     }
     const bool need_mask = partial || (q0 + 15 >= g.n_q) || (k0 + kTileN > g.n_kv) ||
                            !tile_all_visible(g, q0, q_hi_wave, k0, k0 + kTileN - 1);
-    floatx4 fq[DT];                    // this iteration's 64 keys
-#pragma unroll
-    for (int i = 0; i < DT; ++i) fq[i] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
+      floatx4 fq[DT];                  // this subtile's 16 keys, folded in compensated
+#pragma unroll
+      for (int i = 0; i < DT; ++i) fq[i] = floatx4{0.f, 0.f, 0.f, 0.f};
       const int r = rho(t, col);
       const floatx4 s = mfma_f32_dot<KS>([&](int ks) { return sm.k[r * LD + 4 * ks + grp]; },
                                          [&](int ks) { return qf[ks]; });
@@ -737,15 +1169,15 @@ __global__ __launch_bounds__(256, 2) void dq_kernel_32(
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int kr = rho(t, 4 * grp + i);
-        float pv = __builtin_amdgcn_exp2f(s[i] * g.scale_log2 - lse2);
+        float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], g.scale, -lse) * kLog2e);
         if (need_mask && !elem_valid(g, my_q, k0 + kr, partial)) pv = 0.f;
         const float dsv = pv * (dp[i] - dlt) * g.scale;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) fq[dt] = mfma_f32(sm.k[kr * LD + 16 * dt + col], dsv, fq[dt]);
       }
-    }
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) two_sum_fold(dq[dt], cq[dt], fq[dt]);
+      for (int dt = 0; dt < DT; ++dt) two_sum_fold(dq[dt], cq[dt], fq[dt]);
+    }
   }
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) dq[dt] += cq[dt];
@@ -767,19 +1199,31 @@ void launch_delta(const void* o, const void* dout, float* delta, int64_t rows, h
                      (const typename T::storage*)o, (const typename T::storage*)dout, delta, rows);
 }
 
-// dQ first: it also produces Delta, which dK/dV reads
-template <typename T, int D, bool DEFER>
+// dQ first: it also produces -Delta and the base-2 LSE rows, which dK/dV reads
+// from the two halves of the row-term workspace
+template <typename T, int D, bool PRE>
 void launch_bwd16_as(const Geom& g, const void* q, const void* k, const void* v, const void* o,
                      const void* dout, const float* lse, void* dq, void* dk, void* dv, float* delta,
                      const int32_t* row_ptr, const int32_t* row_idx, int n_qt, const int32_t* dq_order,
                      const int32_t* col_ptr, const int32_t* col_idx, const KvWork& w, hipStream_t stream) {
   const int BH = g.B * g.H, BHkv = g.B * g.H_kv;
-  hipLaunchKernelGGL((dq_kernel_16<T, D, DEFER>), dim3(n_qt * BH), dim3(256), 0, stream, g,
-                     (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)o,
-                     (const uint16_t*)dout, (uint16_t*)dq, lse, delta, row_ptr, row_idx, n_qt, dq_order);
-  hipLaunchKernelGGL((dkdv_kernel_16<T, D, DEFER>), dim3(w.n_items * BHkv), dim3(256), 0, stream, g,
-                     (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)dout,
-                     (uint16_t*)dk, (uint16_t*)dv, lse, delta, col_ptr, col_idx, w);
+  const float* lse2 = delta + (size_t)BH * g.n_q;
+  if constexpr (D == 64)
+    hipLaunchKernelGGL((dq_kernel_q64<T, PRE>), dim3(n_qt * BH), dim3(256), 0, stream, g,
+                       (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)o,
+                       (const uint16_t*)dout, (uint16_t*)dq, lse, delta, row_ptr, row_idx, n_qt, dq_order);
+  else
+    hipLaunchKernelGGL((dq_kernel_16<T, D, PRE>), dim3(n_qt * BH), dim3(256), 0, stream, g,
+                       (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)o,
+                       (const uint16_t*)dout, (uint16_t*)dq, lse, delta, row_ptr, row_idx, n_qt, dq_order);
+  if constexpr (D == 64)
+    hipLaunchKernelGGL((dkdv_kernel_q64<T, PRE>), dim3(w.n_items * BHkv), dim3(256), 0, stream, g,
+                       (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)dout,
+                       (uint16_t*)dk, (uint16_t*)dv, lse2, delta, col_ptr, col_idx, w);
+  else
+    hipLaunchKernelGGL((dkdv_kernel_16<T, D, PRE>), dim3(w.n_items * BHkv), dim3(256), 0, stream, g,
+                       (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)dout,
+                       (uint16_t*)dk, (uint16_t*)dv, lse2, delta, col_ptr, col_idx, w);
 }
 
 template <typename T, int D>
@@ -787,7 +1231,7 @@ void launch_bwd16(const Geom& g, const void* q, const void* k, const void* v, co
                   const void* dout, const float* lse, void* dq, void* dk, void* dv, float* delta,
                   const int32_t* row_ptr, const int32_t* row_idx, int n_qt, const int32_t* dq_order,
                   const int32_t* col_ptr, const int32_t* col_idx, const KvWork& w, hipStream_t stream) {
-  if (g.defer_scale)
+  if (g.prescale)
     launch_bwd16_as<T, D, true>(g, q, k, v, o, dout, lse, dq, dk, dv, delta, row_ptr, row_idx, n_qt,
                                 dq_order, col_ptr, col_idx, w, stream);
   else

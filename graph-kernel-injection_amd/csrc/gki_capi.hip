@@ -71,7 +71,7 @@ void set_scale(Geom& g, float scale) {
   g.q_and = scale == 0.f ? 0u : 0xFFFFFFFFu;
   g.q_xor = scale < 0.f ? 0x80008000u : 0u;
   g.qk_scale_log2 = scale == 0.f ? kLog2e : (scale < 0.f ? -scale : scale) * kLog2e;
-  g.defer_scale = 0;   // reference order; make_geom sets it where exact
+  g.prescale = 0;   // reference order; make_geom sets it where exact
 }
 
 int make_geom(Geom& g, int dtype, int B, int H, int H_kv, int n_q, int n_kv, int head_dim,
@@ -102,13 +102,12 @@ int make_geom(Geom& g, int dtype, int B, int H, int H_kv, int n_q, int n_kv, int
   g.n_kv = n_kv;
   g.q_off = n_kv - n_q;
   set_scale(g, scale);
-  // 16-bit backward: cast P (dP - Delta) and scale the fp32 dQ / dK sums when
-  // that gives the same products, i.e. a power-of-two scale on bf16 inputs
-  // (fp32's exponent range, so the unscaled value neither overflows nor
-  // underflows differently); fp16 keeps the reference order, whose cast of the
-  // scaled dS has 1/scale more headroom below the fp16 maximum.
+  // 16-bit backward: the power-of-two scale moves into the dP operand (exact
+  // products; see Geom::prescale) for |scale| in [2^-4, 1]; the dS cast keeps
+  // the reference's place (after the scale) either way.
   int e2 = 0;
-  g.defer_scale = dtype == kBF16 && scale != 0.f && std::fabs(std::frexp(scale, &e2)) == 0.5f;
+  const float mant = std::frexp(scale, &e2);
+  g.prescale = dtype != kF32 && std::fabs(mant) == 0.5f && e2 >= -3 && e2 <= 1;
   g.causal = causal ? 1 : 0;
   g.sink = sink;
   g.window = window;
@@ -125,7 +124,7 @@ int make_geom(Geom& g, int dtype, int B, int H, int H_kv, int n_q, int n_kv, int
 // capture, tight serving loops. Every GPU the library runs on holds its own
 // copy until the process ends. In host code `scratch` names a host-side
 // stand-in, never the device array: the device address comes from
-// hipGetSymbolAddress, once per device (scratch_on_current_device).
+// hipGetSymbolAddress, once per device (scratch_on_device).
 constexpr int64_t kScratchFloats = int64_t(4) << 20;   // 16 MiB
 static __device__ __align__(256) float scratch[kScratchFloats];
 
@@ -133,17 +132,36 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 float* g_scratch_ptr[kMaxDevices] = {};
 
-// The current device's scratch address (looked up on first use per device,
-// with that device current).
-int scratch_on_current_device(float** out) {
-  int dev = -1;
-  const hipError_t e0 = hipGetDevice(&dev);
-  GKI_REQUIRE(e0 == hipSuccess && dev >= 0 && dev < kMaxDevices, 3,
+// The scratch address on the device that `stream` launches on (the current
+// device for the null stream): looked up on first use per device, with that
+// device made current for the lookup and the caller's device restored.
+int scratch_on_device(hipStream_t stream, float** out) {
+  int cur = -1;
+  const hipError_t e0 = hipGetDevice(&cur);
+  GKI_REQUIRE(e0 == hipSuccess && cur >= 0, 3,
               std::string("scratch: no current HIP device (") + hipGetErrorString(e0) + ")");
+  int dev = cur;
+  if (stream != nullptr) {
+    hipDevice_t sd = -1;
+    const hipError_t es = hipStreamGetDevice(stream, &sd);
+    GKI_REQUIRE(es == hipSuccess && sd >= 0, 3,
+                std::string("scratch: hipStreamGetDevice failed: ") + hipGetErrorString(es));
+    dev = (int)sd;
+  }
+  GKI_REQUIRE(dev < kMaxDevices, 3, "scratch: device index " + std::to_string(dev) + " out of range");
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (g_scratch_ptr[dev] == nullptr) {
+    if (dev != cur) {
+      const hipError_t es = hipSetDevice(dev);
+      GKI_REQUIRE(es == hipSuccess, 3, std::string("scratch: hipSetDevice failed: ") + hipGetErrorString(es));
+    }
     void* p = nullptr;
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != cur) {
+      const hipError_t er = hipSetDevice(cur);
+      GKI_REQUIRE(er == hipSuccess, 3,
+                  std::string("scratch: restoring the current device failed: ") + hipGetErrorString(er));
+    }
     GKI_REQUIRE(e == hipSuccess && p != nullptr, 3,
                 std::string("scratch: hipGetSymbolAddress failed: ") + hipGetErrorString(e));
     g_scratch_ptr[dev] = (float*)p;
@@ -206,7 +224,7 @@ using namespace gki;
 
 extern "C" {
 
-int gki_abi_version(void) { return 6; }
+int gki_abi_version(void) { return 7; }
 
 const char* gki_last_error(void) { return g_last_error.c_str(); }
 
@@ -312,7 +330,8 @@ int gki_dkdv_items(const int32_t* col_ptr, int32_t n_kt, int32_t group, int32_t 
   total *= (int64_t)group * bh_kv;
   // iterations per item: at least kDkdvMinChunk, and few enough that the whole
   // grid has about kDkdvTargetItems items of work when columns are long; at
-  // most max_chunk when positive (a shorter fp32 accumulation per item)
+  // most max_chunk when positive (more, shorter items: cuts columns at any
+  // length, e.g. to test the split path on short sequences)
   int64_t chunk = std::max<int64_t>(kDkdvMinChunk, (total + kDkdvTargetItems - 1) / kDkdvTargetItems);
   if (max_chunk > 0) chunk = std::min<int64_t>(chunk, max_chunk);
   int32_t ni = 0, ns = 0, np = 0;
@@ -453,7 +472,7 @@ int gki_rolling_decode_noalloc(const void* q, const void* k_cache, const void* v
                     std::to_string(need) + " floats exceeds the library scratch of " +
                     std::to_string(kScratchFloats) + " floats (16 MiB); use fewer splits or "
                     "gki_rolling_decode with a workspace");
-    if (int rc = scratch_on_current_device(&ws)) return rc;
+    if (int rc = scratch_on_device((hipStream_t)stream, &ws)) return rc;
   }
   return rolling_decode_checked(q, k_cache, v_cache, o, lse, dtype, B, H, H_kv, n_q, head_dim, sink_size,
                                 window_size, ring_size, length, softmax_scale, ws, n_splits, stream);

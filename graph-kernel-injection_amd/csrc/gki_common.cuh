@@ -78,17 +78,21 @@ __device__ inline floatx4 mfma_f32(float a, float b, floatx4 c) {
 
 // fp32 dot products over the head dimension on v_mfma_f32_16x16x4f32, KS
 // k-steps of 4: the steps go round-robin into NC independent accumulators,
-// summed pairwise at the end, so a long contraction (D = 128: 32 steps)
-// rounds like a quarter-length one. a(ks) / b(ks) give step ks's operands.
+// summed pairwise at the end, so a long contraction (D = 64: 16 steps, 2 per
+// accumulator; D = 128: 32 steps, 4 per accumulator) rounds like a short one.
+// With 4 accumulators at D = 64 the scores' and dP's rounding was the largest
+// error of the fp32 gradients at large logits (2x the eager path's on some
+// inputs); 8 halve it. a(ks) / b(ks) give step ks's operands.
 template <int KS, typename FA, typename FB>
 __device__ inline floatx4 mfma_f32_dot(FA a, FB b) {
-  constexpr int NC = KS >= 16 ? 4 : (KS >= 4 ? 2 : 1);
+  constexpr int NC = KS >= 16 ? 8 : (KS >= 8 ? 4 : (KS >= 4 ? 2 : 1));
   floatx4 c[NC];
 #pragma unroll
   for (int j = 0; j < NC; ++j) c[j] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) c[ks % NC] = mfma_f32(a(ks), b(ks), c[ks % NC]);
-  if constexpr (NC == 4) return (c[0] + c[1]) + (c[2] + c[3]);
+  if constexpr (NC == 8) return ((c[0] + c[1]) + (c[2] + c[3])) + ((c[4] + c[5]) + (c[6] + c[7]));
+  else if constexpr (NC == 4) return (c[0] + c[1]) + (c[2] + c[3]);
   else if constexpr (NC == 2) return c[0] + c[1];
   else return c[0];
 }
@@ -113,6 +117,18 @@ __device__ inline uint32_t pack2<BF16>(float a, float b) {
 template <>
 __device__ inline uint32_t pack2<F16>(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, f16x2));
+}
+
+// Eight 16-bit elements times a power-of-two scale, rounded back (exact
+// unless a result falls below the format's smallest normal).
+template <typename T>
+__device__ inline uint4 scale8(const uint4& v, float s) {
+  const uint16_t* h = (const uint16_t*)&v;
+  float f[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) f[i] = T::to_float(h[i]) * s;
+  return make_uint4(pack2<T>(f[0], f[1]), pack2<T>(f[2], f[3]), pack2<T>(f[4], f[5]),
+                    pack2<T>(f[6], f[7]));
 }
 
 // Pack 8 fp32 values into 8 16-bit elements (one 16x16x32 MFMA operand).
@@ -354,12 +370,15 @@ struct Geom {
   // Q K^T * 0) with qk_scale_log2 = log2(e); scale > 0 leaves Q as it is.
   float qk_scale_log2;
   uint32_t q_and, q_xor;
-  // 16-bit backward: dS = P (dP - Delta) scale is cast to 16 bits before the
-  // dK / dQ products. For a power-of-two scale (1/8 at head_dim 64) on bf16
-  // inputs the cast commutes with the scale, so the kernels may cast
-  // P (dP - Delta) and scale the fp32 sums once instead (defer_scale = 1);
-  // otherwise they keep the reference order (defer_scale = 0).
-  int defer_scale;
+  // 16-bit backward: dS = P (dP - Delta) scale, cast to 16 bits before the
+  // dK / dQ products. For a power-of-two scale in [2^-4, 1] (1/8 at
+  // head_dim 64) the kernels multiply the V (dK/dV) or dO (dQ) operand and
+  // -Delta by it once: every product and partial sum of the dP accumulator
+  // is then the same value times the scale (exact in fp32), so it ends as
+  // (dP - Delta) scale and dS costs one multiply (prescale = 1). Only a 16-bit
+  // operand that the scale takes below the smallest normal rounds (by at most
+  // half its subnormal spacing, 2^-25 for fp16). Otherwise prescale = 0.
+  int prescale;
   int causal, sink, window;
   // original block mask (used only for tiles flagged partial)
   const int32_t* mask;
@@ -641,6 +660,15 @@ __device__ inline float wave_sum16x4(float x) {
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_huge_valf();
+
+// The kernels keep each row's running max m2 and sum l in base 2 (scores
+// times log2 e); the stored LSE is the natural log-sum-exp m + ln(l)
+// (sparse_triton_kernel.py:351). Both conversions run once per row in double,
+// so each is a single fp32 rounding of the exact value.
+__device__ inline float lse_natural(float m2, float l) {
+  return (float)(((double)m2 + (double)log2f(l)) * 0.6931471805599453);
+}
+__device__ inline float lse_base2(float lse) { return (float)((double)lse * 1.4426950408889634); }
 
 }  // namespace gki
 

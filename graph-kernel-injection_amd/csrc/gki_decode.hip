@@ -19,9 +19,9 @@
 //     the end, where the waves merge in LDS. With one split per head the workgroup writes O and
 //     LSE itself; otherwise it writes (acc[D], m, l) to a workspace and
 //   * combine_kernel (one wave per row) merges the splits:
-//     O = sum acc_s 2^(m_s-M) / sum l_s 2^(m_s-M), LSE = M + log2 L (base 2,
-//     as the forward stores it), with the (O = 0, LSE = 0) sentinel for empty
-//     rows.
+//     O = sum acc_s 2^(m_s-M) / sum l_s 2^(m_s-M), LSE = (M + log2 L) ln 2
+//     (the partials' max is in base 2; the LSE is natural, as the forward
+//     stores it), with the (O = 0, LSE = 0) sentinel for empty rows.
 // Cross-workgroup merging goes through a second launch on purpose: publishing
 // partials across XCDs inside one kernel needs agent-scope fences, which on
 // gfx950 write back and invalidate L2.
@@ -396,7 +396,7 @@ __global__ __launch_bounds__(64 * decode_waves<NQ>()) void decode_kernel(
     if (n_splits == 1) {
       const bool valid = L > 0.f;
       O[qb + (size_t)r * D + d] = T::from_float(valid ? a / L : 0.f);
-      if (d == 0) LSE[(size_t)bhq0 * g.n_q + r] = valid ? M + log2f(L) : 0.f;
+      if (d == 0) LSE[(size_t)bhq0 * g.n_q + r] = valid ? lse_natural(M, L) : 0.f;
     } else {
       part[r * row_stride + d] = a;
       if (d == 0) {
@@ -440,7 +440,7 @@ __global__ __launch_bounds__(64) void combine_kernel(const float* __restrict__ w
 #pragma unroll
   for (int j = 0; j < D / 64; ++j)
     O[(size_t)row * D + lane + 64 * j] = T::from_float(valid ? a[j] / L : 0.f);
-  if (lane == 0) LSE[row] = valid ? M + log2f(L) : 0.f;
+  if (lane == 0) LSE[row] = valid ? lse_natural(M, L) : 0.f;
 }
 
 template <typename T, int D, int NQ, typename Src>
@@ -724,7 +724,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(
       if (n_splits == 1) {
         const bool valid = L > 0.f;
         O[qb + (size_t)r * D + d] = T::from_float(valid ? a / L : 0.f);
-        if (d == 0) LSE[(size_t)bhq0 * g.n_q + r] = valid ? M + log2f(L) : 0.f;
+        if (d == 0) LSE[(size_t)bhq0 * g.n_q + r] = valid ? lse_natural(M, L) : 0.f;
       } else {
         part[r * row_stride + d] = a;
         if (d == 0) {

@@ -5,10 +5,9 @@
 // reference: S = (Q K^T) * scale in fp32, token mask (causal & (sink | window))
 // inside visited tiles, online softmax, P cast to V's dtype before P V,
 // O = acc / l, LSE = m + log(l) with the (O = 0, LSE = 0) sentinel for rows that
-// saw no key (sparse_triton_kernel.py:341-352). The LSE is stored in base 2
-// (log2 of the row's sum of exp of the scaled scores, i.e. the natural LSE times
-// log2(e)): the running max m is already in base 2 and the backward consumes
-// the base-2 value directly, so no conversion rounds it twice.
+// saw no key (sparse_triton_kernel.py:341-352). The running max m and sum l
+// are kept in base 2 (scores times log2 e, for v_exp_f32); the stored LSE is
+// the natural m + ln(l) of the reference, converted once per row.
 //
 // 16-bit design (one workgroup = 4 waves = one 128-row q tile; wave w owns rows
 // 32w .. 32w+31 as two 16-row blocks h = 0, 1):
@@ -233,13 +232,19 @@ __global__ __launch_bounds__(kFwdThreads, D <= 64 ? 4 : 2) void fwd_kernel_16(
         w.y = pack2<T>(o[h][dt][2] * inv, o[h][dt][3] * inv);
         *(uint2*)(O + qb + (size_t)my_q * D + 16 * dt + 4 * grp) = w;
       }
-      if (grp == 0) LSE[(size_t)bh * g.n_q + my_q] = valid ? m[h] + log2f(l_tot) : 0.f;
+      if (grp == 0) LSE[(size_t)bh * g.n_q + my_q] = valid ? lse_natural(m[h], l_tot) : 0.f;
     }
   }
 }
 
 // ---------------------------------------------------------------------------
 // fp32 path (v_mfma_f32_16x16x4f32, 64-row tiles): K and V stay row-major in LDS.
+// The softmax runs in natural units: the running max m is that of the scaled
+// scores S * scale and each exponent is exp2(fma(S, scale, -m) * log2 e), so
+// the scale is applied exactly and only the (small) difference is rounded;
+// the backward forms P = exp(S * scale - LSE) the same way from the stored
+// LSE = m + ln(l), which therefore matches these scores to within its own
+// rounding.
 // ---------------------------------------------------------------------------
 template <int D>
 struct FwdSmem32 {
@@ -327,26 +332,27 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel_32(
     const bool need_mask = partial || (q0 + 15 >= g.n_q) || (k0 + kTileN > g.n_kv) ||
                            !tile_all_visible(g, q0, q_hi_wave, k0, k0 + kTileN - 1);
     float mx = kNegInf;
+    uint32_t vis = 0xFFFFu;            // bit 4 t + i: element visible
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float x = s[t][i] * g.scale_log2;
-        if (need_mask && !elem_valid(g, my_q, k0 + rho(t, 4 * grp + i), partial)) x = kNegInf;
-        s[t][i] = x;
-        mx = fmaxf(mx, x);
+        const bool ok = !need_mask || elem_valid(g, my_q, k0 + rho(t, 4 * grp + i), partial);
+        if (!ok) vis &= ~(1u << (4 * t + i));
+        mx = fmaxf(mx, ok ? s[t][i] * g.scale : kNegInf);
       }
     }
     mx = wave_max16x4(mx);
     const float m_new = fmaxf(m, mx);
     const float m_use = (m_new == kNegInf) ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m - m_use);
+    const float alpha = __builtin_amdgcn_exp2f((m - m_use) * kLog2e);
     float rs = 0.f;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float p = __builtin_amdgcn_exp2f(s[t][i] - m_use);
+        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][i], g.scale, -m_use) * kLog2e);
+        const float p = (vis >> (4 * t + i)) & 1u ? e : 0.f;
         s[t][i] = p;
         rs += p;
       }
@@ -378,7 +384,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel_32(
       w.w = valid ? o[dt][3] / l_tot : o[dt][3];
       *(float4*)(O + qb + (size_t)my_q * D + 16 * dt + 4 * grp) = w;
     }
-    if (grp == 0) LSE[(size_t)bh * g.n_q + my_q] = valid ? m + log2f(l_tot) : 0.f;
+    if (grp == 0) LSE[(size_t)bh * g.n_q + my_q] = valid ? (float)((double)m + log((double)l_tot)) : 0.f;
   }
 }
 

@@ -13,6 +13,10 @@ from pathlib import Path
 from typing import Optional
 
 LIB_PATH = Path(__file__).resolve().parent / "libgki_bsa.so"
+# The ABI the SIGNATURES table below binds (gki_abi_version() of a matching
+# library). A library built from other sources may export the same names
+# with other argument lists, so load() refuses any other version.
+ABI_VERSION = 7
 
 _c_int = ctypes.c_int32
 _c_i64 = ctypes.c_int64
@@ -70,11 +74,18 @@ def load() -> ctypes.CDLL:
         if _load_error is None:
             try:
                 lib = ctypes.CDLL(str(LIB_PATH))
-                for name, (res, args) in SIGNATURES.items():
-                    fn = getattr(lib, name)
-                    fn.restype = res
-                    fn.argtypes = args
-                _lib = lib
+                lib.gki_abi_version.restype = ctypes.c_int
+                lib.gki_abi_version.argtypes = []
+                found = int(lib.gki_abi_version())
+                if found != ABI_VERSION:
+                    _load_error = (f"{LIB_PATH.name} implements C ABI version {found}, this binding "
+                                   f"needs version {ABI_VERSION} (a stale build)")
+                else:
+                    for name, (res, args) in SIGNATURES.items():
+                        fn = getattr(lib, name)
+                        fn.restype = res
+                        fn.argtypes = args
+                    _lib = lib
             except (OSError, AttributeError) as exc:
                 _load_error = f"{type(exc).__name__}: {exc}"
         if _lib is None:

@@ -166,8 +166,7 @@ class StreamingKVCache:
                 "gki_rolling_decode")
         if not return_lse:
             return o
-        # the kernels store the LSE in base 2; the API returns natural-log units
-        return o, scratch[:B * H * n_q].view(B, H, n_q).mul(math.log(2.0))
+        return o, scratch[:B * H * n_q].view(B, H, n_q).clone()
 
     def step(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
              softmax_scale: Optional[float] = None) -> torch.Tensor:

@@ -256,7 +256,8 @@ class _BlockSparseFlashAttention(torch.autograd.Function):
         dq = torch.empty_like(q)
         dk = torch.empty_like(k)
         dv = torch.empty_like(v)
-        delta = torch.empty((B, H, N_Q), dtype=torch.float32, device=q.device)
+        # row terms: Delta, then the base-2 LSE rows (internal to the backward)
+        delta = torch.empty((2, B, H, N_Q), dtype=torch.float32, device=q.device)
         with _on_device(q.device):
             stream = _current_stream(q.device)
             sched = bwd_schedule(block_mask, N_Q, N_KV, ctx.block_m, ctx.block_n, ctx.is_causal,

@@ -5,12 +5,12 @@
  * Conventions
  *  - Tensors are device pointers to contiguous [B, H, N, D] arrays (BHND,
  *    row-major), as produced by `.contiguous()` in the reference
- *    (sparse_triton_kernel.py:834). LSE / Delta are contiguous fp32 [B, H, N_Q].
- *  - LSE is stored in base 2: log2 of each row's sum of exp of its scaled
- *    scores, i.e. the natural log-sum-exp times log2(e) (0 for rows that see
- *    no key, as the reference's sentinel, sparse_triton_kernel.py:341-352).
- *    The kernels keep the running max in base 2 and the backward consumes the
- *    value as is, so it is rounded once instead of three times.
+ *    (sparse_triton_kernel.py:834). LSE is contiguous fp32 [B, H, N_Q].
+ *  - LSE is the reference's: the natural log of each row's sum of exp of its
+ *    scaled scores, m + ln(l) (sparse_triton_kernel.py:351), 0 for rows that
+ *    see no key (its sentinel, :341-352). The kernels keep the running max in
+ *    base 2 and convert once per row (in double, one fp32 rounding); the
+ *    backward converts the stored value back once per row.
  *  - Grouped-query attention: Q / O / dQ have H heads, K / V / dK / dV have
  *    H_kv heads, H_kv dividing H; q head h reads kv head h / (H / H_kv).
  *    H_kv == H is the reference's multi-head case (the reference rejects any
@@ -42,9 +42,11 @@
 extern "C" {
 #endif
 
-/* ABI version (currently 6: grouped-query attention, H_kv after H; dK/dV work
+/* ABI version (currently 7: grouped-query attention, H_kv after H; dK/dV work
  * items from gki_dkdv_items, whose chunk can be capped by max_chunk; the
- * optional workgroup orders of the forward and dQ grids from gki_fwd_order). */
+ * optional workgroup orders of the forward and dQ grids from gki_fwd_order;
+ * natural-log LSE in every output; gki_bsa_bwd's row-term workspace holds
+ * 2 * B * H * N_Q floats). */
 int gki_abi_version(void);
 
 /* Message of the last failing call on this thread. */
@@ -101,9 +103,11 @@ int gki_block_list_fill(const int32_t* m, int32_t n_rows, int32_t n_cols,
  * col_ptr: the CSC column pointers (n_kt + 1, host copy) of the backward tiles;
  * group: q heads per K/V head; bh_kv: B * H_kv. A kv tile's walk of
  * group x (its list length) iterations becomes one item, or -- when longer than
- * the chunk max(32, ceil(total iterations / 8192)), capped at max_chunk when
- * max_chunk > 0 -- several near-equal items whose fp32 partials gki_bsa_bwd
- * sums in item order (deterministic; fp32 partials with a compensated sum). Writes
+ * the chunk max(32, ceil(total iterations / 8192)) -- several near-equal items
+ * whose fp32 partials gki_bsa_bwd sums in item order (deterministic; fp32
+ * partials with a compensated sum). max_chunk > 0 caps the chunk (more,
+ * shorter items: a caller may cut columns of any length, as the tests do to
+ * run the split path on short sequences); 0 keeps the rule above. Writes
  * items [n_items][4] = (kv tile, first iteration, end iteration, partial slot or
  * -1) and split [n_split][3] = (kv tile, first slot, slot count), and the counts;
  * pass items = split = NULL to size them first. n_pslots partial slots per
@@ -124,7 +128,7 @@ int gki_fwd_order(const int32_t* row_ptr, int32_t n_qt, int32_t bh, int32_t* ord
 
 /* Prefill forward: replaces the `_fwd_kernel` launch in
  * `_BlockSparseFlashAttention.forward` (sparse_triton_kernel.py:662-682).
- * O = softmax(mask(Q K^T * scale)) V, LSE (base 2) = m + log2(l), 0 for empty rows.
+ * O = softmax(mask(Q K^T * scale)) V, LSE = m + ln(l) (natural), 0 for empty rows.
  * row_ptr/row_idx: CSR over ceil(n_q/fwd_tile_m) q tiles (fwd_tile_m_16 or
  * fwd_tile_m_32 by dtype) of kept kv tiles. wg_order: NULL (index order) or a
  * device copy of gki_fwd_order's table for this CSR and B * H (a workgroup
@@ -141,9 +145,10 @@ int gki_bsa_fwd(const void* q, const void* k, const void* v, void* o, float* lse
  * over the CSC list (device copies of gki_dkdv_items' lists: kv_items 16-byte
  * aligned; kv_partials a 16-byte aligned fp32 workspace
  * [B * H_kv][n_pslots][2][64][head_dim], needed when n_split > 0) and dQ over
- * the CSR list, both over bwd_tile_m x tile_n tiles. `delta` is a caller-owned fp32
- * [B, H, N_Q] workspace for the row terms (its contents on return are internal:
- * Delta for fp32 inputs, -Delta for fp16 / bf16). dq, dk, dv are
+ * the CSR list, both over bwd_tile_m x tile_n tiles. `lse` is the forward's
+ * (natural) LSE. `delta` is a caller-owned fp32 [2, B, H, N_Q] workspace for
+ * the row terms (its contents on return are internal: Delta -- negated and
+ * scaled for fp16 / bf16 -- then each row's LSE in base 2). dq, dk, dv are
  * fully written (no zero-fill needed). dq_order: NULL (index order) or a
  * device copy of gki_fwd_order's table for the backward CSR and B * H (the
  * dQ grid runs each XCD's q tiles longest list first). */
@@ -239,7 +244,8 @@ int gki_rolling_decode(const void* q, const void* k_cache, const void* v_cache, 
  * (other streams, other threads) share the array and race; serialise them.
  * No counterpart in the reference: it is for callers that cannot allocate
  * (code under HIP graph capture, tight serving loops, harnesses that forbid
- * allocation). */
+ * allocation). The array used is that of the device `stream` launches on (the
+ * current device for the null stream), looked up once per device. */
 int gki_rolling_decode_noalloc(const void* q, const void* k_cache, const void* v_cache, void* o,
                                float* lse, int32_t dtype, int32_t B, int32_t H, int32_t H_kv,
                                int32_t n_q, int32_t head_dim, int32_t sink_size,

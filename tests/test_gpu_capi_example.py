@@ -2,7 +2,7 @@
 (hipMalloc'd buffers, no Python or torch in the process) builds the StreamingLLM
 mask, the forward tile classes and the CSR schedule with the library, runs
 ``gki_bsa_fwd`` on a ragged bf16 shape (N = 300, not a multiple of any tile) and
-checks O and the base-2 LSE against a double-precision attention over the token
+checks O and the (natural) LSE against a double-precision attention over the token
 rule computed in the same program (O within 2e-2 + 1e-2 |ref|, LSE within
 2.5e-3); a schedule of the wrong size must be rejected. ``build()`` links the
 program against the in-tree library."""

@@ -16,12 +16,13 @@ gradients ~20) are outside the range those fixed bounds were set for, so the
 case also runs the reference's own eager path (``reference_block_sparse_attention``,
 sparse_triton_kernel.py:845-902, in the input dtype on the CPU, gradients by
 autograd) as a control: every element of the kernel's result must lie within
-max(the fixed tolerance, 2 x the eager path's worst error on the same tensor)
-of the fp64 oracle. At these magnitudes the fp32 rounding of the scores Q K^T
+max(the fixed tolerance, 2 x the eager path's error on the same tensor) of the
+fp64 oracle. At these magnitudes the fp32 rounding of the scores Q K^T
 dominates every result, so the eager path's own error moves by up to ~3x with
-the order of the head-dimension sum alone; the control therefore takes its
-worst error over four such orders (the identity and three fixed permutations
-of the head dimension of Q and K, which leave the mathematics unchanged).
+the order of the head-dimension sum alone; the control's error is therefore
+the median of its maximum errors over four such orders (the identity and three
+fixed permutations of the head dimension of Q and K, which leave the
+mathematics unchanged): a typical eager run, not its worst.
 """
 
 from __future__ import annotations
@@ -63,19 +64,18 @@ def _case(seed):
                 mask_seed=int(rng.integers(0, 1 << 30)))
 
 
-def _close(ours, ref, dtype, what, eager=None):
+def _close(ours, ref, dtype, what, e_err=None):
     """Element-wise |ours - ref| <= atol + rtol |ref|, widened to twice the
-    eager control's worst error on the same tensor when one is given."""
+    eager control's (median) maximum error on the same tensor when given."""
     o = ours.detach().to(torch.float64).cpu()
     r = torch.as_tensor(ref).to(torch.float64)
     assert torch.isfinite(o).all(), what
     atol, rtol = TOL[dtype]
     bound = atol + rtol * r.abs()
     info = f"max err {(o - r).abs().max():.3e}, max |ref| {r.abs().max():.3e}"
-    if eager is not None:
-        e_err = float((eager.detach().to(torch.float64).cpu() - r).abs().max())
+    if e_err is not None:
         bound = bound.clamp_min(2.0 * e_err)
-        info += f", eager control max err {e_err:.3e}"
+        info += f", eager control max err (median of 4 orders) {e_err:.3e}"
     bad = (o - r).abs() > bound
     assert not bad.any(), f"{what}: {int(bad.sum())} out of tolerance, {info}"
 
@@ -98,19 +98,17 @@ def _eager_once(q, k, v, do, mask, group, c, perm):
 
 
 def _eager_control(q, k, v, do, mask, group, c, refs):
-    """Per result tensor, the eager path's run with the largest error against
-    ``refs`` over four head-dimension orders (see the module docstring)."""
+    """Per result tensor, the median over four head-dimension orders (see the
+    module docstring) of the eager path's maximum error against ``refs``."""
     D = q.shape[-1]
     rng = np.random.default_rng(D)
     perms = [torch.arange(D)] + [torch.from_numpy(rng.permutation(D)) for _ in range(3)]
-    worst = [None] * 4
+    errs = [[] for _ in range(4)]
     for perm in perms:
         res = _eager_once(q, k, v, do, mask, group, c, perm)
         for i, (t, r) in enumerate(zip(res, refs)):
-            err = float((t.to(torch.float64) - torch.as_tensor(r)).abs().max())
-            if worst[i] is None or err > worst[i][0]:
-                worst[i] = (err, t)
-    return [w[1] for w in worst]
+            errs[i].append(float((t.to(torch.float64) - torch.as_tensor(r)).abs().max()))
+    return [float(np.median(e)) for e in errs]
 
 
 @pytest.mark.gpu

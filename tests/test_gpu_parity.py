@@ -43,16 +43,20 @@ def _close(ours: torch.Tensor, ref: torch.Tensor, dtype: torch.dtype, what: str)
                            f"{float(err.max()):.3e}, worst excess={float((err - bound).max()):.3e}")
 
 
-def _inputs(shape_q, shape_kv, dtype, seed, scale=1.0, device_gen=False, grad_out=False):
-    if device_gen:
-        g = torch.Generator(device=DEV).manual_seed(seed)
-        mk = lambda s: (torch.randn(s, generator=g, device=DEV, dtype=torch.float32) * scale).to(dtype)
+def _inputs(shape_q, shape_kv, dtype, seed, scale=1.0, chunked=False, grad_out=False):
+    """q, k, v (and dO) ~ N(0, scale^2) from a CPU generator seeded per case,
+    then moved to the GPU: the same bits on every host. ``chunked`` draws
+    through ``benchmark.seeded_normal`` (per-chunk CPU generators on a thread
+    pool), for the full-size decode and layer configs, as bench.py does."""
+    shapes = [shape_q, shape_kv, shape_kv] + ([shape_q] if grad_out else [])
+    if chunked:
+        from benchmark import seeded_normal
+
+        ts = seeded_normal(shapes, seed, dtype, DEV, scale=scale)
     else:
         g = torch.Generator().manual_seed(seed)
-        mk = lambda s: (torch.randn(s, generator=g, dtype=torch.float32) * scale).to(dtype).to(DEV)
-    q, k, v = mk(shape_q), mk(shape_kv), mk(shape_kv)
-    do = mk(shape_q) if grad_out else None
-    return q, k, v, do
+        ts = [(torch.randn(s, generator=g, dtype=torch.float32) * scale).to(dtype).to(DEV) for s in shapes]
+    return ts[0], ts[1], ts[2], (ts[3] if grad_out else None)
 
 
 # ---------------------------------------------------------------------------
@@ -395,12 +399,13 @@ def test_lse_vs_oracle(case, dtype, bar):
 
 
 def _forward_lse(q, k, v, mask, bm, bn, S, W):
-    """LSE saved for backward by the autograd Function, in natural-log units
-    (the kernels store it in base 2)."""
+    """LSE saved for backward by the autograd Function: the reference's natural
+    m + ln(l) (sparse_triton_kernel.py:351, saved at :684), as the kernels
+    store it."""
     leaves = [t.detach().requires_grad_(True) for t in (q, k, v)]
     out = stk.block_sparse_attention(*leaves, mask, block_m=bm, block_n=bn, is_causal=True,
                                      sink_size=S, window_size=W)
-    return out.grad_fn.saved_tensors[4].double() * math.log(2.0)
+    return out.grad_fn.saved_tensors[4].double()
 
 
 @pytest.mark.parametrize("dtype,chunk", [(torch.float32, 1), (torch.float32, 5),
@@ -435,7 +440,7 @@ def test_dkdv_any_cut_of_the_work_list_matches_oracle(chunk, dtype):
     split_d = torch.from_numpy(split if len(split) else np.zeros((1, 3), np.int32)).to(DEV)
     partials = torch.empty(max(B * H_kv * n_pslots * 2 * 64 * D, 1), dtype=torch.float32, device=DEV)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-    delta = torch.empty((B, H, N), dtype=torch.float32, device=DEV)
+    delta = torch.empty((2, B, H, N), dtype=torch.float32, device=DEV)   # row-term workspace
     code = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}[dtype]
     n_b = (N + bm - 1) // bm
     lib = _lib.load()
@@ -473,7 +478,7 @@ def test_config3_train_fp16_full():
 
 def test_config4_decode_bf16_full():
     B, H, NKV, D, S, W = 8, 32, 100000, 128, 4, 2048
-    q, k, v, _ = _inputs((B, H, 1, D), (B, H, NKV, D), torch.bfloat16, seed=3, device_gen=True)
+    q, k, v, _ = _inputs((B, H, 1, D), (B, H, NKV, D), torch.bfloat16, seed=3, chunked=True)
     mask = stk.make_streaming_mask(1, NKV, stk.StreamingMaskSpec(S, W), 1, 64, device=DEV)
     out = stk.block_sparse_attention(q, k, v, mask, block_m=1, block_n=64, is_causal=True,
                                      sink_size=S, window_size=W)
@@ -484,7 +489,7 @@ def test_config4_decode_bf16_full():
 def test_config5_layer_bf16_full():
     """One c5 attention layer (1x16x131072x64, S4 W4096, 128x64 blocks), fwd+bwd."""
     B, H, N, D, S, W, bm, bn = 1, 16, 131072, 64, 4, 4096, 128, 64
-    q, k, v, do = _inputs((B, H, N, D), (B, H, N, D), torch.bfloat16, seed=4, device_gen=True,
+    q, k, v, do = _inputs((B, H, N, D), (B, H, N, D), torch.bfloat16, seed=4, chunked=True,
                           grad_out=True)
     mask = stk.make_streaming_mask(N, N, stk.StreamingMaskSpec(S, W), bm, bn, device=DEV)
     leaves = [t.clone().requires_grad_(True) for t in (q, k, v)]
@@ -602,7 +607,7 @@ def test_dq_order_gives_the_index_order_bits(dtype):
     L = sched.lists
     partials = torch.empty(max(B * H * sched.n_pslots * 2 * 64 * D, 1), dtype=torch.float32, device=DEV)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-    delta = torch.empty((B, H, N), dtype=torch.float32, device=DEV)
+    delta = torch.empty((2, B, H, N), dtype=torch.float32, device=DEV)   # row-term workspace
     n_b = (N + bm - 1) // bm
     lib = _lib.load()
     rc = lib.gki_bsa_bwd(

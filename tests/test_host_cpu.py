@@ -104,7 +104,24 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(lib, name), f"{name} declared in gki_bsa.h but not exported"
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
     assert set(_lib.SIGNATURES) == set(names)
-    assert lib.gki_abi_version() == 6
+    assert lib.gki_abi_version() == _lib.ABI_VERSION == 7
+
+
+def test_load_refuses_other_abi_version(monkeypatch):
+    """A library whose gki_abi_version differs from the binding's table (a stale
+    build exporting the same names with other argument lists) is refused with a
+    RuntimeError naming both versions, as the reference raises when its backend
+    is unusable (sparse_triton_kernel.py:626-630); nothing is bound from it."""
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "_load_error", None)
+    monkeypatch.setattr(_lib, "ABI_VERSION", 6)
+    with pytest.raises(RuntimeError, match=r"C ABI version 7, this binding needs version 6"):
+        _lib.load()
+    assert not _lib.available()
+    # the real binding loads again once the expected version matches
+    monkeypatch.setattr(_lib, "_load_error", None)
+    monkeypatch.setattr(_lib, "ABI_VERSION", 7)
+    assert _lib.load().gki_abi_version() == 7
 
 
 def test_dkdv_work_list_matches_oracle():

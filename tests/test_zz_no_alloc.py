@@ -1,8 +1,9 @@
 """gki_rolling_decode_noalloc (the allocation-free decode entry point) against
 gki_rolling_decode with a caller workspace, through the C ABI: bit-identical
 O and LSE on two calls in a row, the second smaller, on both decode kernels
-(grouped-query rows on the matrix cores, single rows on the vector decode),
-and a clear error, before any launch, for a request beyond the 16 MiB scratch."""
+(grouped-query rows on the matrix cores, single rows on the vector decode);
+no change of the device's free memory over repeated calls; and a clear error,
+before any launch, for a request beyond the 16 MiB scratch."""
 
 from __future__ import annotations
 
@@ -58,6 +59,41 @@ def test_noalloc_decode_equals_the_workspace_decode_twice():
 def test_noalloc_decode_single_split_and_positions():
     _case(2, 8, 8, 3, 128, 900, 4, 256, 1, seed=63, dtype=torch.float16)
     _case(2, 8, 2, 2, 64, 900, 4, 256, 2, seed=64, dtype=torch.float16)
+
+
+def test_noalloc_decode_allocates_nothing():
+    """The entry point's defining contract: after a warm-up call (which loads the
+    code object holding the scratch array), further calls with preallocated
+    outputs leave the device's free memory unchanged -- no hipMalloc, no
+    allocating library routine, on the split path (4 splits, the scratch) and
+    on the single-split path."""
+    lib = _lib.load()
+    B, H, H_kv, n_q, D, length, S, W = 2, 16, 4, 1, 128, 5000, 4, 1024
+    ring = W + n_q - 1
+    g = torch.Generator().manual_seed(65)
+    q = torch.randn(B, H, n_q, D, generator=g).to(torch.bfloat16).to(DEV)
+    kc = torch.randn(B, H_kv, S + ring, D, generator=g).to(torch.bfloat16).to(DEV)
+    vc = torch.randn(B, H_kv, S + ring, D, generator=g).to(torch.bfloat16).to(DEV)
+    o = torch.empty_like(q)
+    lse = torch.empty(B, H, n_q, dtype=torch.float32, device=DEV)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def call(n_splits):
+        rc = lib.gki_rolling_decode_noalloc(q.data_ptr(), kc.data_ptr(), vc.data_ptr(), o.data_ptr(),
+                                            lse.data_ptr(), 2, B, H, H_kv, n_q, D, S, W, ring, length,
+                                            1.0 / math.sqrt(D), n_splits, stream)
+        assert rc == 0, lib.gki_last_error()
+
+    for n_splits in (4, 1):          # warm-up: code objects loaded, scratch address looked up
+        call(n_splits)
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    for _ in range(20):
+        for n_splits in (4, 1):
+            call(n_splits)
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info()[0] == free0
+    assert torch.isfinite(o).all() and torch.isfinite(lse).all()
 
 
 def test_noalloc_decode_rejects_requests_beyond_the_scratch():
