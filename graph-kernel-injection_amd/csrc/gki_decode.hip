@@ -543,21 +543,27 @@ __device__ inline void vm_wait() {
 #endif
 template <int D>
 constexpr int decode_mfma_bufs() { return GKI_DECODE_MFMA_BUFS; }
-template <int D>
-constexpr int decode_mfma_lds() { return 2 * decode_mfma_bufs<D>() * kTileN * D * 2; }
-
-// Wait until at most k chunks (of 2 * NP LDS-DMA instructions per wave each)
-// are still in flight.
-template <int NP, int NBUF>
-__device__ inline void wait_chunks(int k) {
-  static_assert(NBUF <= 4, "wait_chunks covers up to three chunks in flight");
-  if (k <= 0) vm_wait<0>();
-  else if (k == 1) vm_wait<2 * NP>();
-  else if (k == 2) vm_wait<(NBUF > 2 ? 4 * NP : 0)>();
-  else vm_wait<(NBUF > 3 ? 6 * NP : 0)>();
+// K / V ring, plus the workgroup's query rows (at most 2 * kDecodeTileM) when
+// they are staged through LDS (QLDS).
+template <int D, bool QLDS>
+constexpr int decode_mfma_lds() {
+  return 2 * decode_mfma_bufs<D>() * kTileN * D * 2 + (QLDS ? 2 * kDecodeTileM * D * 2 : 0);
 }
 
-template <typename T, int D, bool EXACT, int NB>
+// Wait until at most k chunks (of 2 * NP LDS-DMA instructions per wave each,
+// k <= NBUF) are still in flight: every memory operation issued before them
+// has completed.
+template <int NP, int NBUF>
+__device__ inline void wait_chunks(int k) {
+  static_assert(NBUF <= 4 && 8 * NP < 64, "wait_chunks covers up to four chunks in flight");
+  if (k <= 0) vm_wait<0>();
+  else if (k == 1) vm_wait<2 * NP>();
+  else if (k == 2) vm_wait<4 * NP>();
+  else if (k == 3) vm_wait<6 * NP>();
+  else vm_wait<8 * NP>();
+}
+
+template <typename T, int D, bool EXACT, int NB, bool QLDS>
 __global__ __launch_bounds__(256) void decode_mfma_kernel(
     Geom g, const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const uint16_t* __restrict__ V, uint16_t* __restrict__ O, float* __restrict__ LSE,
@@ -569,6 +575,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(
   extern __shared__ __align__(16) uint16_t decode_lds[];
   uint16_t* const sk = decode_lds;                       // [NBUF][64 * D]
   uint16_t* const sv = decode_lds + NBUF * kTileN * D;   // [NBUF][64 * D]
+  uint16_t* const sq = decode_lds + 2 * NBUF * kTileN * D;   // [n_rows][D], row-major
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -584,19 +591,33 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(
   const int n_chunks = (g1 - g0 + kTileN - 1) / kTileN;
 
   // Q^T operand of column block h: lane (grp, col) holds elements 32ks + 8grp ..
-  // +7 of q row 16h + col
+  // +7 of q row 16h + col. QLDS (a split stream: a short slice, where the start
+  // weighs): the workgroup's n_rows query rows, contiguous in Q, are staged into
+  // LDS by LDS-DMA ahead of the first K / V chunks (1 KB per wave instruction;
+  // lanes past the rows re-read the last 16 bytes, landing in LDS no row uses),
+  // so their latency overlaps the K / V stream instead of preceding it;
+  // otherwise (a long slice) they are loaded into registers first.
   uint4 qf[NB][KS];
+  if constexpr (QLDS) {
+    const int q_bytes = n_rows * D * 2;
+#pragma unroll
+    for (int j = wave; j < (2 * kDecodeTileM * D * 2) / 1024; j += 4)
+      if (j * 1024 < q_bytes)
+        dma_load16((const char*)(Q + qb) + min(j * 1024 + 16 * lane, q_bytes - 16), lds_addr(sq) + j * 1024);
+  } else {
+#pragma unroll
+    for (int h = 0; h < NB; ++h) {
+      const int r = 16 * h + col;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        qf[h][ks] = r < n_rows ? q_words(g, *(const uint4*)(Q + qb + (size_t)r * D + 32 * ks + 8 * grp))
+                               : make_uint4(0, 0, 0, 0);
+    }
+    dma_wait();   // the Q loads are complete before any LDS-DMA is in flight
+  }
   int my_q[NB];                                             // the lane's query position index
 #pragma unroll
-  for (int h = 0; h < NB; ++h) {
-    const int r = 16 * h + col;
-    my_q[h] = r % g.n_q;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      qf[h][ks] = r < n_rows ? q_words(g, *(const uint4*)(Q + qb + (size_t)r * D + 32 * ks + 8 * grp))
-                             : make_uint4(0, 0, 0, 0);
-  }
-  dma_wait();   // the Q loads are complete before any LDS-DMA is in flight
+  for (int h = 0; h < NB; ++h) my_q[h] = (16 * h + col) % g.n_q;
 
   // this lane's chunk of LDS block 4p + wave of a tile: row, swizzled column
   int drow[NP], dcol[NP];
@@ -633,6 +654,21 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(
 #pragma unroll
   for (int c = 0; c < NBUF; ++c)
     if (c < n_chunks) issue(c, c);
+  if constexpr (QLDS) {
+    // the Q rows have landed once at most the chunks just issued are in flight
+    // (vector memory operations complete in order); every wave's share of
+    // them is visible after the barrier
+    wait_chunks<NP, NBUF>(min(NBUF, n_chunks));
+    __syncthreads();
+#pragma unroll
+    for (int h = 0; h < NB; ++h) {
+      const int r = 16 * h + col;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        qf[h][ks] = r < n_rows ? q_words(g, *(const uint4*)(sq + r * D + 32 * ks + 8 * grp))
+                               : make_uint4(0, 0, 0, 0);
+    }
+  }
   for (int c = 0; c < n_chunks; ++c) {
     const int b = c % NBUF;
     // chunk c has landed; the up to NBUF - 1 chunks issued after it may stay in flight
@@ -751,31 +787,32 @@ int launch_decode_mfma(const Geom& g, const void* q, const void* k, const void* 
                        const RingTokens& src, int kv_rows, int n_tokens, float* ws, int n_splits,
                        hipStream_t stream, const char* what) {
   const int n_wgh = g.B * g.H_kv;
-  constexpr int lds = decode_mfma_lds<D>();
-  if constexpr (lds > 65536) {
+  constexpr int lds_q = decode_mfma_lds<D, true>(), lds_r = decode_mfma_lds<D, false>();
+  if constexpr (lds_q > 65536 || lds_r > 65536) {
     // above the 64 KB default: opt in once per device and instantiation
     static std::atomic<uint64_t> done{0};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return fail(3, std::string(what) + ": hipGetDevice failed");
     const uint64_t bit = dev < 64 ? (1ull << dev) : 0;
     if (!bit || !(done.load() & bit)) {
-      if (hipFuncSetAttribute((const void*)decode_mfma_kernel<T, D, true, 1>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess ||
-          hipFuncSetAttribute((const void*)decode_mfma_kernel<T, D, false, 1>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess ||
-          hipFuncSetAttribute((const void*)decode_mfma_kernel<T, D, true, 2>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess ||
-          hipFuncSetAttribute((const void*)decode_mfma_kernel<T, D, false, 2>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
-        return fail(3, std::string(what) + ": cannot reserve LDS for the matrix-core decode");
+      bool ok = true;
+#define GKI_MFMA_LDS(EX, NBK, QL, BYTES)                                                            ok = ok && (BYTES <= 65536 || hipFuncSetAttribute((const void*)decode_mfma_kernel<T, D, EX, NBK, QL>,                                                     hipFuncAttributeMaxDynamicSharedMemorySize,                                                           BYTES) == hipSuccess)
+      GKI_MFMA_LDS(true, 1, true, lds_q);
+      GKI_MFMA_LDS(false, 1, true, lds_q);
+      GKI_MFMA_LDS(true, 2, true, lds_q);
+      GKI_MFMA_LDS(false, 2, true, lds_q);
+      GKI_MFMA_LDS(true, 1, false, lds_r);
+      GKI_MFMA_LDS(false, 1, false, lds_r);
+      GKI_MFMA_LDS(true, 2, false, lds_r);
+      GKI_MFMA_LDS(false, 2, false, lds_r);
+#undef GKI_MFMA_LDS
+      if (!ok) return fail(3, std::string(what) + ": cannot reserve LDS for the matrix-core decode");
       done.fetch_or(bit);
     }
   }
   const int n_rows = g.group * g.n_q;
-#define GKI_MFMA_DECODE(EX, NBK)                                                            \
-  hipLaunchKernelGGL((decode_mfma_kernel<T, D, EX, NBK>), dim3(n_wgh * n_splits), dim3(256), lds, \
-                     stream, g, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,      \
-                     (uint16_t*)o, lse, ws, src, kv_rows, n_tokens, n_splits)
+  // split streams (short slices) stage their query rows through LDS
+#define GKI_MFMA_DECODE(EX, NBK)                                                                   do {                                                                                             if (n_splits > 1)                                                                                hipLaunchKernelGGL((decode_mfma_kernel<T, D, EX, NBK, true>), dim3(n_wgh * n_splits),                            dim3(256), lds_q, stream, g, (const uint16_t*)q, (const uint16_t*)k,                            (const uint16_t*)v, (uint16_t*)o, lse, ws, src, kv_rows, n_tokens,                              n_splits);                                                                else                                                                                             hipLaunchKernelGGL((decode_mfma_kernel<T, D, EX, NBK, false>), dim3(n_wgh * n_splits),                           dim3(256), lds_r, stream, g, (const uint16_t*)q, (const uint16_t*)k,                            (const uint16_t*)v, (uint16_t*)o, lse, ws, src, kv_rows, n_tokens,                              n_splits);                                                              } while (0)
   if (n_rows <= kDecodeTileM) {
     if (g.n_q == 1) GKI_MFMA_DECODE(true, 1);
     else GKI_MFMA_DECODE(false, 1);
