@@ -24,6 +24,8 @@
 //    barrier per tile, the next tile's global loads in flight during the MFMAs.
 //  * Only kept tiles are visited (GPU-resident CSR list); the O^T rescale is
 //    skipped, exactly, when no row max of a block moved.
+//  * head_dim 128 runs the loop skewed by one kv tile (fwd_kernel_16's PIPE),
+//    so that one wave's MFMAs of the next tile overlap its own softmax.
 //  * The running max is kept on unscaled scores, so Q is read through the
 //    Geom::q_and / q_xor transform that makes the effective scale positive.
 // The fp32 path uses v_mfma_f32_16x16x4f32 on 64-row tiles (16 rows per wave).
@@ -48,12 +50,38 @@ constexpr float kNoMax = -3.40282347e38f;
 // (eight waves, twice the waves per SIMD at head_dim 128) was 10% slower: the
 // doubled LDS reads per MFMA cost more than the occupancy gained.
 constexpr int kFwdRB = 2;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+// Issue order of the skewed (PIPE) loop, imposed with sched_group_barrier
+// (masks: 0x008 MFMA, 0x100 LDS read, 0x002 VALU). S_{j+1}: kPipeAheadS K
+// reads first, then per MFMA pair one more read and kPipeValu1 + kPipeValu2
+// VALU ops of the exp work between the two MFMAs and after them. O += V P:
+// kPipeAheadO V^T reads first, then two reads and one VALU op (the maxima of
+// S_{j+1}) per MFMA pair. Measured on the c2 forward: 2 + 1 VALU beat 3 + 2
+// by 1.5%; reads 4 / 8 ahead beat 2 / 4 by 1.6%; without the imposed order
+// the compiler issues every MFMA first and the loop is 5% slower than this.
+constexpr int kPipeAheadS = 4, kPipeAheadO = 8, kPipeValu1 = 2, kPipeValu2 = 1;
 constexpr int kFwdThreads = 64 * (8 / kFwdRB);
-// Workgroups per CU the compiler must fit in registers: 4 (up to 128 VGPRs) for
-// head_dim <= 64, whose 32 KB of K / V buffers allow four workgroups per CU (the
-// extra waves hide more latency: 4-7% faster than three at head_dim 64); 2 for
-// head_dim 128 (64 KB of buffers).
-template <typename T, int D>
+// Waves per SIMD the compiler must fit in registers (HIP's second launch
+// bound): 4 (up to 128 VGPRs) for head_dim <= 64, whose 32 KB of K / V buffers
+// allow four workgroups per CU (the extra waves hide more latency: 4-7% faster
+// than three at head_dim 64); 2 for head_dim 128 (64 KB of buffers, two
+// workgroups per CU). Eight-wave workgroups over 256-row q tiles (half the K /
+// V staging per flop) ran 6-13% slower at both head dims.
+//
+// PIPE selects the tile schedule. Without it every kv tile runs S = K Q^T,
+// then mask / max / exp, then O += V P in turn, and the matrix cores idle
+// through the softmax unless the SIMD's other wave has MFMAs to issue. With
+// it the loop is skewed by one tile: iteration j runs S_{j+1} = K_{j+1} Q^T
+// while it exponentiates S_j (MFMA and VALU of one wave in one straight-line
+// block, interleaved in the order kPipe* describes), then O += V_j P_j while
+// it takes the row maxima of S_{j+1}. K is therefore read one tile ahead of V:
+// at iteration j the LDS holds K_{j+1} and V_j while K_{j+2} and V_{j+1} land
+// in the other halves of the two double buffers (the same 2 x 2 tiles of LDS).
+// The loop is unrolled by two so that the two score tiles swap roles without
+// register copies, and P_j is pinned (an empty asm that takes it) inside the
+// S_{j+1} block: otherwise the compiler sinks the exp work past the mask
+// branch into the O += V P block and no MFMA of S_{j+1} overlaps it.
+template <typename T, int D, bool PIPE>
 __global__ __launch_bounds__(kFwdThreads, D <= 64 ? 4 : 2) void fwd_kernel_16(
     Geom g, const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const uint16_t* __restrict__ V, uint16_t* __restrict__ O, float* __restrict__ LSE,
@@ -112,39 +140,23 @@ __global__ __launch_bounds__(kFwdThreads, D <= 64 ? 4 : 2) void fwd_kernel_16(
   dma.init(tid);
   // Full tiles go LDS-DMA; the ragged last kv tile goes through registers so
   // that its out-of-range rows are zero (P = 0 must not meet stale V).
-  auto stage = [&](int k0, int b) {
+  auto stage1 = [&](const uint16_t* src, int k0, uint16_t* dst) {
     if (k0 + kTileN <= g.n_kv) {
-      dma.load(K + kb, k0, sk[b]);
-      dma.load(V + kb, k0, sv[b]);
+      dma.load(src + kb, k0, dst);
     } else {
       RowTile<D, NT> t;
-      t.load(K + kb, k0, g.n_kv, tid);
-      t.store(sk[b], tid);
-      t.load(V + kb, k0, g.n_kv, tid);
-      t.store(sv[b], tid);
+      t.load(src + kb, k0, g.n_kv, tid);
+      t.store(dst, tid);
       // Unconditional, so that no register load of this branch is pending
       // where it rejoins the DMA path: otherwise the compiler waits for all
       // vector memory there, the just-issued DMA of the next tile included.
       dma_wait();
     }
   };
+  auto tile_k0 = [&](int ent) { return (ent & kIdxMask) * kTileN; };
 
-  const int e_beg = row_ptr[qt], e_end = row_ptr[qt + 1];
-  if (e_beg < e_end) stage((row_idx[e_beg] & kIdxMask) * kTileN, 0);
-  dma_wait();
-  __syncthreads();
-
-  for (int e = e_beg; e < e_end; ++e) {
-    const int buf = (e - e_beg) & 1;
-    const int ent = row_idx[e];
-    const int k0 = (ent & kIdxMask) * kTileN;
-    const bool partial = (ent >> kPartialBit) & 1;
-    if (e + 1 < e_end) stage((row_idx[e + 1] & kIdxMask) * kTileN, buf ^ 1);
-    const uint16_t* ck = sk[buf];
-    const uint16_t* cv = sv[buf];
-
-    floatx4 s[RB][4];
-    mfma_priority_hi<(D <= 64)>();
+  // S^T of one kv tile for both row blocks.
+  auto scores = [&](const uint16_t* ck, floatx4 (&s)[RB][4]) {
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
 #pragma unroll
@@ -158,52 +170,73 @@ __global__ __launch_bounds__(kFwdThreads, D <= 64 ? 4 : 2) void fwd_kernel_16(
         for (int h = 0; h < RB; ++h) s[h][t] = T::mfma(a, qf[h][ks], s[h][t]);
       }
     }
-
-    mfma_priority_lo<(D <= 64)>();
+  };
+  // Token mask of row block h of a tile (only where some element of it can
+  // be hidden).
+  auto apply_mask = [&](int ent, int h, floatx4 (&s)[4]) {
+    const int k0 = tile_k0(ent);
+    const bool partial = (ent >> kPartialBit) & 1;
+    const int q0 = qw + 16 * h;
+    const bool need_mask = partial || (q0 + 15 >= g.n_q) || (k0 + kTileN > g.n_kv) ||
+                           !tile_all_visible(g, q0, min(q0 + 15, g.n_q - 1), k0, k0 + kTileN - 1);
+    if (need_mask) {
+      const LaneBits vis(row_valid_bits(g, q0 + col, k0, partial), grp);
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[t][i] = vis.pick(t, i, s[t][i], kNegInf);
+    }
+  };
+  auto lane_max = [&](const floatx4 (&s)[4]) {
+    float mx = kNegInf;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[t][i]);
+    return mx;
+  };
+  // A row's max exceeds the reference by the slack only if one of its lanes'
+  // maxima does (qk_scale_log2 > 0, so scaling after the max is exact): the
+  // cross-lane reduction runs only then. The threshold is a trigger only:
+  // whether m moves is decided exactly inside. Rescales O and the row sums of
+  // block h, so it runs after every product of the tiles before.
+  auto move_max = [&](int h, float mx) {
+    if (__any(mx > thr[h])) {
+      const float mr = wave_max16x4(mx) * g.qk_scale_log2;
+      const bool grow = mr > m[h] + kRescaleSlack;
+      const float alpha = grow ? __builtin_amdgcn_exp2f(m[h] - mr) : 1.f;
+      m[h] = grow ? mr : m[h];
+      thr[h] = (m[h] + kRescaleSlack) * inv_c;
+      lsum[h][0] *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) o[h][dt] *= alpha;
+    }
+  };
+  // P = exp2(S c - m) of row block h, in place.
+  auto exp_h = [&](int h, floatx4 (&s)[4]) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        s[t][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][i], g.qk_scale_log2, -m[h]));
+  };
+  // P of both row blocks packed to 16-bit MFMA operands (subtiles 2st, 2st+1).
+  auto probs = [&](floatx4 (&s)[RB][4], uint4 (&p)[2][RB]) {
 #pragma unroll
     for (int h = 0; h < RB; ++h) {
-      const int q0 = qw + 16 * h;
-      const bool need_mask = partial || (q0 + 15 >= g.n_q) || (k0 + kTileN > g.n_kv) ||
-                             !tile_all_visible(g, q0, min(q0 + 15, g.n_q - 1), k0, k0 + kTileN - 1);
-      if (need_mask) {
-        const LaneBits vis(row_valid_bits(g, q0 + col, k0, partial), grp);
+      exp_h(h, s[h]);
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) s[h][t][i] = vis.pick(t, i, s[h][t][i], kNegInf);
-      }
-      float mx = kNegInf;
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[h][t][i]);
-      // A row's max exceeds the reference by the slack only if one of its
-      // lanes' maxima does (qk_scale_log2 > 0, so scaling after the max is
-      // exact): the cross-lane reduction runs only then. The threshold is a
-      // trigger only: whether m moves is decided exactly inside.
-      if (__any(mx > thr[h])) {
-        mx = wave_max16x4(mx) * g.qk_scale_log2;
-        const bool grow = mx > m[h] + kRescaleSlack;
-        const float alpha = grow ? __builtin_amdgcn_exp2f(m[h] - mx) : 1.f;
-        m[h] = grow ? mx : m[h];
-        thr[h] = (m[h] + kRescaleSlack) * inv_c;
-        lsum[h][0] *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) o[h][dt] *= alpha;
-      }
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          s[h][t][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[h][t][i], g.qk_scale_log2, -m[h]));
+      for (int st = 0; st < 2; ++st) p[st][h] = pack8<T>(s[h][2 * st], s[h][2 * st + 1]);
     }
-
-    mfma_priority_hi<(D <= 64)>();
+  };
+  // O^T += V^T P^T and the row sums; operand(st, h) gives P of subtiles
+  // (2st, 2st+1) of row block h.
+  auto accumulate = [&](const uint16_t* cv, auto&& operand) {
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
       uint4 b[RB];
 #pragma unroll
-      for (int h = 0; h < RB; ++h) b[h] = pack8<T>(s[h][2 * st], s[h][2 * st + 1]);
+      for (int h = 0; h < RB; ++h) b[h] = operand(st, h);
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
         const uint4 a = lds_tr8<D>(cv, 32 * st, 16 * dt, lane);
@@ -213,9 +246,141 @@ __global__ __launch_bounds__(kFwdThreads, D <= 64 ? 4 : 2) void fwd_kernel_16(
 #pragma unroll
       for (int h = 0; h < RB; ++h) lsum[h] = T::mfma(ones, b[h], lsum[h]);
     }
-    mfma_priority_lo<(D <= 64)>();
-    dma_wait();        // the next tile's LDS-DMA has landed before the barrier
+  };
+  // K and V of one tile into buffer b (the ragged tile with one wait).
+  auto stage2 = [&](int k0, int b) {
+    if (k0 + kTileN <= g.n_kv) {
+      dma.load(K + kb, k0, sk[b]);
+      dma.load(V + kb, k0, sv[b]);
+    } else {
+      RowTile<D, NT> t;
+      t.load(K + kb, k0, g.n_kv, tid);
+      t.store(sk[b], tid);
+      t.load(V + kb, k0, g.n_kv, tid);
+      t.store(sv[b], tid);
+      dma_wait();
+    }
+  };
+
+  const int e_beg = row_ptr[qt], e_end = row_ptr[qt + 1];
+  if constexpr (!PIPE) {
+    if (e_beg < e_end) stage2(tile_k0(row_idx[e_beg]), 0);
+    dma_wait();
     __syncthreads();
+
+    for (int e = e_beg; e < e_end; ++e) {
+      const int buf = (e - e_beg) & 1;
+      const int ent = row_idx[e];
+      if (e + 1 < e_end) stage2(tile_k0(row_idx[e + 1]), buf ^ 1);
+      floatx4 s[RB][4];
+      mfma_priority_hi<(D <= 64)>();
+      scores(sk[buf], s);
+      mfma_priority_lo<(D <= 64)>();
+#pragma unroll
+      for (int h = 0; h < RB; ++h) {
+        apply_mask(ent, h, s[h]);
+        move_max(h, lane_max(s[h]));
+        exp_h(h, s[h]);
+      }
+      mfma_priority_hi<(D <= 64)>();
+      accumulate(sv[buf], [&](int st, int h) { return pack8<T>(s[h][2 * st], s[h][2 * st + 1]); });
+      mfma_priority_lo<(D <= 64)>();
+      dma_wait();        // the next tile's LDS-DMA has landed before the barrier
+      __syncthreads();
+    }
+  } else {
+    const int n = e_end - e_beg;
+    floatx4 sa[RB][4], sb[RB][4];
+    // Prologue: K_0, V_0 and K_1 in LDS, S_0 with its maxima.
+    if (n > 0) {
+      const int k0 = tile_k0(row_idx[e_beg]);
+      stage1(K, k0, sk[0]);
+      stage1(V, k0, sv[0]);
+      if (n > 1) stage1(K, tile_k0(row_idx[e_beg + 1]), sk[1]);
+    }
+    dma_wait();
+    __syncthreads();
+    if (n > 0) {
+      const int ent = row_idx[e_beg];
+      scores(sk[0], sa);
+#pragma unroll
+      for (int h = 0; h < RB; ++h) {
+        apply_mask(ent, h, sa[h]);
+        move_max(h, lane_max(sa[h]));
+      }
+    }
+    __syncthreads();   // every wave is done with K_0 before iteration 0 refills its buffer
+
+    // Iteration j (j + 1 < n): S_{j+1} from K_{j+1} into sn while s = S_j
+    // becomes P_j; O += V_j P_j while sn's maxima are taken.
+    auto step = [&](int j, floatx4 (&s)[RB][4], floatx4 (&sn)[RB][4]) {
+      const int e = e_beg + j;
+      const int ent1 = row_idx[e + 1];
+      // LDS: K_{j+1} in sk[(j+1)&1], V_j in sv[j&1]; refill the other halves
+      if (j + 2 < n) stage1(K, tile_k0(row_idx[e + 2]), sk[j & 1]);
+      stage1(V, tile_k0(ent1), sv[(j + 1) & 1]);
+
+      uint4 p[2][RB];
+      scores(sk[(j + 1) & 1], sn);   // MFMA ...
+      probs(s, p);                   // ... under VALU
+      // P is formed here, not sunk past the mask branch into the next block
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int h = 0; h < RB; ++h) {
+          u32x4 w = __builtin_bit_cast(u32x4, p[st][h]);
+          asm volatile("" : "+v"(w));
+          p[st][h] = __builtin_bit_cast(uint4, w);
+        }
+      // issue order: the MFMAs of S_{j+1} (4 KS RB, in pairs) between the exp work
+      __builtin_amdgcn_sched_group_barrier(0x100, kPipeAheadS, 0);
+#pragma unroll
+      for (int i = 0; i < 2 * KS * RB; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (i + kPipeAheadS < 4 * KS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, kPipeValu1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, kPipeValu2, 0);
+      }
+#pragma unroll
+      for (int h = 0; h < RB; ++h) apply_mask(ent1, h, sn[h]);
+      accumulate(sv[j & 1], [&](int st, int h) { return p[st][h]; });   // MFMA ...
+      float mx[RB];
+#pragma unroll
+      for (int h = 0; h < RB; ++h) mx[h] = lane_max(sn[h]);   // ... under VALU
+      // issue order: the 2 DT MFMA pairs of O += V P (two V^T reads each) with
+      // the maxima of S_{j+1} between them
+      __builtin_amdgcn_sched_group_barrier(0x100, kPipeAheadO, 1);
+#pragma unroll
+      for (int i = 0; i < 2 * DT; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+        if (2 * i + kPipeAheadO < 4 * DT) __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+        __builtin_amdgcn_sched_group_barrier(0x002, 1, 1);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+        if (2 * i + 1 + kPipeAheadO < 4 * DT) __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+      }
+#pragma unroll
+      for (int h = 0; h < RB; ++h) move_max(h, mx[h]);
+      dma_wait();
+      __syncthreads();
+    };
+    auto last = [&](floatx4 (&s)[RB][4]) {
+      uint4 p[2][RB];
+      probs(s, p);
+      accumulate(sv[(n - 1) & 1], [&](int st, int h) { return p[st][h]; });
+    };
+    // Unrolled by two so that the score buffers swap roles without copies.
+    int j = 0;
+    for (; j + 2 < n; j += 2) {
+      step(j, sa, sb);
+      step(j + 1, sb, sa);
+    }
+    if (j + 1 < n) {
+      step(j, sa, sb);
+      last(sb);
+    } else if (n > 0) {
+      last(sa);
+    }
   }
 
 #pragma unroll
@@ -388,6 +553,13 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel_32(
   }
 }
 
+// The skewed schedule holds two score tiles (32 more VGPRs): head_dim 128
+// has them within its 256; at head_dim 64 it would cost the fourth workgroup
+// per CU (168 VGPRs), and three skewed workgroups ran 2-7% slower than four
+// plain ones (c3 / c5 forward).
+template <int D>
+constexpr bool kFwdPipe = D >= 128;
+
 template <int D>
 int launch_fwd(int dtype, const Geom& g, const void* q, const void* k, const void* v, void* o,
                float* lse, const int32_t* row_ptr, const int32_t* row_idx, int n_qt,
@@ -398,11 +570,11 @@ int launch_fwd(int dtype, const Geom& g, const void* q, const void* k, const voi
                        (const float*)k, (const float*)v, (float*)o, lse, row_ptr, row_idx, n_qt,
                        wg_order);
   } else if (dtype == kF16) {
-    hipLaunchKernelGGL((fwd_kernel_16<F16, D>), dim3(grid), dim3(kFwdThreads), 0, stream, g,
+    hipLaunchKernelGGL((fwd_kernel_16<F16, D, kFwdPipe<D>>), dim3(grid), dim3(kFwdThreads), 0, stream, g,
                        (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, lse,
                        row_ptr, row_idx, n_qt, wg_order);
   } else {
-    hipLaunchKernelGGL((fwd_kernel_16<BF16, D>), dim3(grid), dim3(kFwdThreads), 0, stream, g,
+    hipLaunchKernelGGL((fwd_kernel_16<BF16, D, kFwdPipe<D>>), dim3(grid), dim3(kFwdThreads), 0, stream, g,
                        (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, lse,
                        row_ptr, row_idx, n_qt, wg_order);
   }
