@@ -1064,27 +1064,31 @@ __global__ __launch_bounds__(256, 4) void dq_kernel_q64(
     __syncthreads();
   }
   // the kv-half sums meet in LDS (the K buffers are free: every wave passed the
-  // loop's last barrier): kh = 1 waves store, kh = 0 waves add theirs first
+  // loop's last barrier): kh = 1 waves store, kh = 0 waves add theirs first.
+  // Row offsets from the lane index afresh (mbcnt: not provably the one
+  // above), not the prologue's held (spilled) across the loop.
+  const int lane_e = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+  const int grp_e = lane_e >> 4, col_e = lane_e & 15;
   floatx4* red = (floatx4*)&sk[0][0] + qh * (2 * DT * 64);
   if (kh == 1) {
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) red[(b * DT + dt) * 64 + lane] = dq[b][dt];
+      for (int dt = 0; dt < DT; ++dt) red[(b * DT + dt) * 64 + lane_e] = dq[b][dt];
   }
   __syncthreads();
   if (kh == 1) return;
 #pragma unroll
   for (int b = 0; b < 2; ++b) {
-    const int my_q = q0w + 16 * b + col;
+    const int my_q = q0w + 16 * b + col_e;
     if (my_q >= g.n_q) continue;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
-      const floatx4 o = red[(b * DT + dt) * 64 + lane];
+      const floatx4 o = red[(b * DT + dt) * 64 + lane_e];
       uint2 w;
       w.x = pack2<T>(dq[b][dt][0] + o[0], dq[b][dt][1] + o[1]);
       w.y = pack2<T>(dq[b][dt][2] + o[2], dq[b][dt][3] + o[3]);
-      *(uint2*)(dQ + qb + (size_t)my_q * D + 16 * dt + 4 * grp) = w;
+      *(uint2*)(dQ + qb + (size_t)my_q * D + 16 * dt + 4 * grp_e) = w;
     }
   }
 }

@@ -101,8 +101,8 @@ __global__ __launch_bounds__(kFwdThreads, D <= 64 ? 4 : 2) void fwd_kernel_16(
   const int bh = wg / n_qt, qt = wg - bh * n_qt;
   const size_t qb = (size_t)bh * g.n_q * D;
   const size_t kb = (size_t)kv_bh(g, bh) * g.n_kv * D;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int grp = lane >> 4, col = lane & 15;
+  const int tid = threadIdx.x, wave = tid >> 6;
+  const int lane = tid & 63, grp = lane >> 4, col = lane & 15;
   const int qw = qt * kTileMF + wave * 16 * RB;   // first row of this wave
 
   uint4 qf[RB][KS];
@@ -271,19 +271,65 @@ __global__ __launch_bounds__(kFwdThreads, D <= 64 ? 4 : 2) void fwd_kernel_16(
     for (int e = e_beg; e < e_end; ++e) {
       const int buf = (e - e_beg) & 1;
       const int ent = row_idx[e];
+      const int k0 = tile_k0(ent);
+      const bool partial = (ent >> kPartialBit) & 1;
       if (e + 1 < e_end) stage2(tile_k0(row_idx[e + 1]), buf ^ 1);
+      const uint16_t* ck = sk[buf];
+      const uint16_t* cv = sv[buf];
+
       floatx4 s[RB][4];
       mfma_priority_hi<(D <= 64)>();
-      scores(sk[buf], s);
+      scores(ck, s);
       mfma_priority_lo<(D <= 64)>();
 #pragma unroll
       for (int h = 0; h < RB; ++h) {
-        apply_mask(ent, h, s[h]);
-        move_max(h, lane_max(s[h]));
-        exp_h(h, s[h]);
+        const int q0 = qw + 16 * h;
+        const bool need_mask = partial || (q0 + 15 >= g.n_q) || (k0 + kTileN > g.n_kv) ||
+                               !tile_all_visible(g, q0, min(q0 + 15, g.n_q - 1), k0, k0 + kTileN - 1);
+        if (need_mask) {
+          const LaneBits vis(row_valid_bits(g, q0 + col, k0, partial), grp);
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s[h][t][i] = vis.pick(t, i, s[h][t][i], kNegInf);
+        }
+        float mx = kNegInf;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[h][t][i]);
+        if (__any(mx > thr[h])) {
+          mx = wave_max16x4(mx) * g.qk_scale_log2;
+          const bool grow = mx > m[h] + kRescaleSlack;
+          const float alpha = grow ? __builtin_amdgcn_exp2f(m[h] - mx) : 1.f;
+          m[h] = grow ? mx : m[h];
+          thr[h] = (m[h] + kRescaleSlack) * inv_c;
+          lsum[h][0] *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) o[h][dt] *= alpha;
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            s[h][t][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[h][t][i], g.qk_scale_log2, -m[h]));
       }
+
       mfma_priority_hi<(D <= 64)>();
-      accumulate(sv[buf], [&](int st, int h) { return pack8<T>(s[h][2 * st], s[h][2 * st + 1]); });
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        uint4 b[RB];
+#pragma unroll
+        for (int h = 0; h < RB; ++h) b[h] = pack8<T>(s[h][2 * st], s[h][2 * st + 1]);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const uint4 a = lds_tr8<D>(cv, 32 * st, 16 * dt, lane);
+#pragma unroll
+          for (int h = 0; h < RB; ++h) o[h][dt] = T::mfma(a, b[h], o[h][dt]);
+        }
+#pragma unroll
+        for (int h = 0; h < RB; ++h) lsum[h] = T::mfma(ones, b[h], lsum[h]);
+      }
       mfma_priority_lo<(D <= 64)>();
       dma_wait();        // the next tile's LDS-DMA has landed before the barrier
       __syncthreads();
@@ -383,9 +429,13 @@ __global__ __launch_bounds__(kFwdThreads, D <= 64 ? 4 : 2) void fwd_kernel_16(
     }
   }
 
+  // The epilogue's row offsets from the lane index afresh (mbcnt: not provably
+  // the one above), not the prologue's Q offsets held across the loop.
+  const int lane_e = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+  const int grp_e = lane_e >> 4, col_e = lane_e & 15;
 #pragma unroll
   for (int h = 0; h < RB; ++h) {
-    const int my_q = qw + 16 * h + col;
+    const int my_q = qw + 16 * h + col_e;
     const float l_tot = lsum[h][0];
     const bool valid = l_tot > 0.f;
     const float inv = valid ? 1.f / l_tot : 1.f;
@@ -395,9 +445,9 @@ __global__ __launch_bounds__(kFwdThreads, D <= 64 ? 4 : 2) void fwd_kernel_16(
         uint2 w;
         w.x = pack2<T>(o[h][dt][0] * inv, o[h][dt][1] * inv);
         w.y = pack2<T>(o[h][dt][2] * inv, o[h][dt][3] * inv);
-        *(uint2*)(O + qb + (size_t)my_q * D + 16 * dt + 4 * grp) = w;
+        *(uint2*)(O + qb + (size_t)my_q * D + 16 * dt + 4 * grp_e) = w;
       }
-      if (grp == 0) LSE[(size_t)bh * g.n_q + my_q] = valid ? lse_natural(m[h], l_tot) : 0.f;
+      if (grp_e == 0) LSE[(size_t)bh * g.n_q + my_q] = valid ? lse_natural(m[h], l_tot) : 0.f;
     }
   }
 }
