@@ -231,6 +231,17 @@ SMALL = [
 ]
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("n_kv", [64, 100, 128, 192, 256, 300, 320, 384])
+def test_fwd_d128_kept_tile_counts(n_kv, dtype):
+    """head_dim 128 runs the 16-bit forward skewed by one kv tile and unrolled
+    by two (the next tile's S while the current one's softmax runs, a peeled
+    last step for odd counts). One 128-row q tile that sees every key (a
+    window past n_kv) keeps ceil(n_kv / 64) kv tiles: 1 .. 6 here, even and
+    odd, with a ragged last tile at 100 and 300 keys."""
+    _run_case(1, 2, 128, n_kv, 128, dtype, 64, 64, True, 4, 4096, seed=n_kv, backward=False)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("case", SMALL, ids=lambda c: "x".join(map(str, c)))
 def test_small_causal_vs_oracle(case, dtype):
