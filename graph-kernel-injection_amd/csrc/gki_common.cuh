@@ -234,6 +234,18 @@ struct RowTile {
   }
 };
 
+// 16 bytes at (row, d0) of a row-major [n_rows, D] 16-bit matrix, zero when
+// row >= n_rows or d0 >= D (n_rows >= 1). The load is unconditional, from a
+// clamped in-bounds address, and the zero a select: as a predicated load each
+// would sit in its own branch with its own wait, so that a kernel prologue's
+// row loads would land one after another instead of together.
+template <int D>
+__device__ inline uint4 row16_or_zero(const uint16_t* base, int row, int n_rows, int d0) {
+  const bool ok = row < n_rows && d0 < D;
+  const uint4 v = *(const uint4*)(base + (size_t)min(row, n_rows - 1) * D + (d0 < D ? d0 : 0));
+  return ok ? v : make_uint4(0, 0, 0, 0);
+}
+
 // LDS byte address of a pointer into __shared__ memory.
 __device__ inline uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
