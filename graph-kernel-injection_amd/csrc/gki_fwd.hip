@@ -112,8 +112,8 @@ __global__ __launch_bounds__(kFwdThreads, D <= 64 ? 4 : 2) void fwd_kernel_16(
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const int d0 = 32 * ks + 8 * grp;
-      qf[h][ks] = (q < g.n_q && d0 < D) ? q_words(g, *(const uint4*)(Q + qb + (size_t)q * D + d0))
-                                        : make_uint4(0, 0, 0, 0);
+      const uint4 v = q_words(g, row16_or_zero<D>(Q + qb, q, g.n_q, d0));
+      qf[h][ks] = (q < g.n_q && d0 < D) ? v : make_uint4(0, 0, 0, 0);
     }
   }
 
