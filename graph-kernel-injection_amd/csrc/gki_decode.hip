@@ -537,12 +537,10 @@ __device__ inline void vm_wait() {
   __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
 }
 
-// Chunks in flight per workgroup (LDS ring of K and V tiles).
-#ifndef GKI_DECODE_MFMA_BUFS
-#define GKI_DECODE_MFMA_BUFS 2
-#endif
+// Chunks in flight per workgroup (LDS ring of K and V tiles): three or four
+// measured no faster than two on the grouped-query and four-position steps.
 template <int D>
-constexpr int decode_mfma_bufs() { return GKI_DECODE_MFMA_BUFS; }
+constexpr int decode_mfma_bufs() { return 2; }
 // K / V ring, plus the workgroup's query rows (at most 2 * kDecodeTileM) when
 // they are staged through LDS (QLDS).
 template <int D, bool QLDS>
