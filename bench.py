@@ -285,12 +285,50 @@ def section_c4(steps: int, warmup: int, cpu_sample: Optional[dict] = None) -> di
     log(f"[c4] decode step after evicting the memory-side cache: {cold * 1e3:.2f} us, "
         f"{res['cold_cache']['kv_gbs']:.0f} GB/s ({100 * res['cold_cache']['frac']:.1f}% of HBM peak)")
     res["rolling_cache"] = _rolling_c4(q, k, v, S, W, fn(), exact_bytes, steps, warmup)
+    res["read_ceiling"] = _read_ceiling_c4(k, v, S, W, exact_bytes, avg, cold, steps, warmup)
     if cpu_sample is not None:      # the whole step for the CPU leg (13 GB of bf16 K / V on the host)
         cpu_sample["c4"] = (q.cpu(), k.cpu(), v.cpu(), mask.cpu())
     del k, v
     res["gqa"] = _gqa_c4(B, H, NKV, D, S, W, mask, steps, warmup)
     res["multi_query"] = _gqa_c4(B, H, NKV, D, S, W, mask, steps, warmup, H_kv=1)
     res["four_positions"] = _gqa_c4(B, H, NKV, D, S, W, mask, steps, warmup, H_kv=H, n_q=4)
+    return res
+
+
+def _read_ceiling_c4(k, v, S, W, exact_bytes, decode_ms, decode_cold_ms, steps, warmup) -> dict:
+    """The read ceiling of the c4 step's own access pattern: ``gki_read_probe``
+    streams exactly its token-exact K / V rows (the sink rows and the window
+    rows of every (b, h) slice) with 16-byte non-temporal loads and no other
+    work, timed like the step: back to back, and after the 2 GiB read that
+    evicts the memory-side cache. ``decode_share`` = probe time / step time."""
+    import torch
+
+    from gki import _lib
+
+    lib = _lib.load()
+    B, H, NKV, D = k.shape
+    bh = B * H
+    words = int(lib.gki_read_probe_words(bh))
+    out = torch.empty(words, dtype=torch.int32, device=k.device)
+    row_bytes = D * k.element_size()
+
+    def fn():
+        stream = torch.cuda.current_stream(k.device).cuda_stream
+        _lib.check(lib.gki_read_probe(k.data_ptr(), v.data_ptr(), bh, NKV, row_bytes, S, W, out.data_ptr(),
+                                      words, stream), "gki_read_probe")
+
+    avg, _ = _time_calls(fn, steps, warmup)
+    cold = _time_cold(fn)
+    res = {"protocol": "gki_read_probe over the same token-exact rows (8 chunks x 256 threads x 4 "
+                       "non-temporal 16-byte loads per window, one workgroup for the sink rows); "
+                       "warm: back-to-back calls; cold: as decode.cold_cache",
+           "warm_ms": avg, "cold_ms": cold,
+           "warm_frac_of_hbm": exact_bytes / (avg * 1e-3) / 1e9 / PEAK_HBM,
+           "cold_frac_of_hbm": exact_bytes / (cold * 1e-3) / 1e9 / PEAK_HBM,
+           "decode_share_warm": avg / decode_ms, "decode_share_cold": cold / decode_cold_ms}
+    log(f"[c4] read ceiling of the step's rows: {avg * 1e3:.2f} us warm ({100 * res['warm_frac_of_hbm']:.1f}% "
+        f"of HBM peak), {cold * 1e3:.2f} us cold ({100 * res['cold_frac_of_hbm']:.1f}%); the decode step "
+        f"reaches {100 * res['decode_share_warm']:.1f}% / {100 * res['decode_share_cold']:.1f}% of it")
     return res
 
 

@@ -52,6 +52,9 @@ int decode_ring_dispatch(int dtype, int head_dim, const Geom& g, const void* q, 
                          hipStream_t stream);
 int append_dispatch(int dtype, int head_dim, void* kc, void* vc, const void* kn, const void* vn, int BH,
                     int n_new, int start, int sink, int ring, hipStream_t stream);
+int64_t read_probe_words(int BH);
+int read_probe_dispatch(const void* k, const void* v, int BH, int64_t n_kv, int row_bytes, int n_sink,
+                        int64_t w_lo, uint32_t* out, hipStream_t stream);
 
 namespace {
 
@@ -224,7 +227,7 @@ using namespace gki;
 
 extern "C" {
 
-int gki_abi_version(void) { return 7; }
+int gki_abi_version(void) { return 8; }
 
 const char* gki_last_error(void) { return g_last_error.c_str(); }
 
@@ -476,6 +479,22 @@ int gki_rolling_decode_noalloc(const void* q, const void* k_cache, const void* v
   }
   return rolling_decode_checked(q, k_cache, v_cache, o, lse, dtype, B, H, H_kv, n_q, head_dim, sink_size,
                                 window_size, ring_size, length, softmax_scale, ws, n_splits, stream);
+}
+
+int64_t gki_read_probe_words(int32_t bh) { return bh > 0 ? read_probe_words(bh) : 0; }
+
+int gki_read_probe(const void* k, const void* v, int32_t bh, int64_t n_kv, int32_t row_bytes,
+                   int32_t sink_size, int32_t window_size, uint32_t* out, int64_t out_words, void* stream) {
+  GKI_REQUIRE(k && v && out, 1, "gki_read_probe: null pointer");
+  GKI_REQUIRE(all_aligned16(k, v), 1, "gki_read_probe: k and v must be 16-byte aligned");
+  GKI_REQUIRE(bh >= 1 && bh <= (1 << 26) && n_kv >= 1 && row_bytes >= 16 && row_bytes % 16 == 0, 1,
+              "gki_read_probe: bh and n_kv must be positive, row_bytes a positive multiple of 16");
+  GKI_REQUIRE(sink_size >= 0 && window_size >= 0, 1, "gki_read_probe: sink_size and window_size must be >= 0");
+  GKI_REQUIRE(out_words >= read_probe_words(bh), 1,
+              "gki_read_probe: out must hold gki_read_probe_words(bh) words");
+  const int n_sink = (int)std::min<int64_t>(sink_size, n_kv);
+  const int64_t w_lo = std::max<int64_t>(n_sink, n_kv - window_size);
+  return read_probe_dispatch(k, v, bh, n_kv, row_bytes, n_sink, w_lo, out, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -945,4 +945,60 @@ int append_dispatch(int dtype, int head_dim, void* kc, void* vc, const void* kn,
   return launch_append_t<BF16>(head_dim, kc, vc, kn, vn, BH, n_new, n_a, i_b, n_b, start, sink, ring, stream);
 }
 
+// ---------------------------------------------------------------------------
+// Read probe (measurement only): the bytes a single-position StreamingLLM
+// decode step reads -- per (b, kv head) slice the sink rows 0 .. n_sink - 1 and
+// the window rows w_lo .. n_kv - 1 of K and of V -- streamed with 16-byte
+// non-temporal loads and XOR-folded into one word per thread (so no load can be
+// dropped), with no other work: the ceiling of that access pattern, timed by
+// bench.py beside the decode step. Workgroup (slice, tensor, part): parts
+// 0 .. kReadParts - 1 split the window rows into near-equal chunks, the last
+// part reads the sink rows; kReadUnroll loads in flight per thread. (Eight
+// chunks of 256 threads with four loads each was the fastest of ten layouts
+// measured on the c4 rows with the memory-side cache evicted.)
+// ---------------------------------------------------------------------------
+typedef uint32_t probe_u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kReadParts = 8;
+constexpr int kReadUnroll = 4;
+constexpr int kReadThreads = 256;
+
+__global__ __launch_bounds__(kReadThreads) void read_probe_kernel(
+    const probe_u32x4* __restrict__ k, const probe_u32x4* __restrict__ v, int64_t slice16, int64_t sink16,
+    int64_t win_lo16, int64_t win16, uint32_t* __restrict__ out) {
+  const int part = blockIdx.x % (kReadParts + 1);
+  const int t = (blockIdx.x / (kReadParts + 1)) & 1;
+  const int64_t s = blockIdx.x / (2 * (kReadParts + 1));
+  const probe_u32x4* base = (t ? v : k) + s * slice16;
+  int64_t lo = 0, n = sink16;
+  if (part < kReadParts) {
+    const int64_t c = (win16 + kReadParts - 1) / kReadParts;
+    lo = win_lo16 + part * c;
+    n = win16 - part * c < c ? win16 - part * c : c;
+    n = n > 0 ? n : 0;
+  }
+  probe_u32x4 acc = {0u, 0u, 0u, 0u};
+  for (int64_t i = threadIdx.x; i < n; i += (int64_t)kReadThreads * kReadUnroll) {
+    probe_u32x4 r[kReadUnroll];
+#pragma unroll
+    for (int u = 0; u < kReadUnroll; ++u) {
+      const int64_t j = i + (int64_t)u * kReadThreads;
+      r[u] = j < n ? __builtin_nontemporal_load(base + lo + j) : probe_u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int u = 0; u < kReadUnroll; ++u) acc ^= r[u];
+  }
+  out[(int64_t)blockIdx.x * kReadThreads + threadIdx.x] = acc.x ^ acc.y ^ acc.z ^ acc.w;
+}
+
+int64_t read_probe_words(int BH) { return (int64_t)BH * 2 * (kReadParts + 1) * kReadThreads; }
+
+int read_probe_dispatch(const void* k, const void* v, int BH, int64_t n_kv, int row_bytes, int n_sink,
+                        int64_t w_lo, uint32_t* out, hipStream_t stream) {
+  const int64_t r16 = row_bytes / 16;
+  hipLaunchKernelGGL(read_probe_kernel, dim3(BH * 2 * (kReadParts + 1)), dim3(kReadThreads), 0, stream,
+                     (const probe_u32x4*)k, (const probe_u32x4*)v, n_kv * r16, (int64_t)n_sink * r16,
+                     w_lo * r16, (n_kv - w_lo) * r16, out);
+  return check_launch("gki_read_probe");
+}
+
 }  // namespace gki

@@ -16,7 +16,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libgki_bsa.so"
 # The ABI the SIGNATURES table below binds (gki_abi_version() of a matching
 # library). A library built from other sources may export the same names
 # with other argument lists, so load() refuses any other version.
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _c_int = ctypes.c_int32
 _c_i64 = ctypes.c_int64
@@ -56,6 +56,9 @@ SIGNATURES = {
                                                                        _c_int, _c_ptr]),
     "gki_rolling_decode_noalloc": (ctypes.c_int, [_c_ptr] * 5 + [_c_int] * 9
                                    + [_c_i64, _c_float, _c_int, _c_ptr]),
+    "gki_read_probe_words": (ctypes.c_int64, [_c_int]),
+    "gki_read_probe": (ctypes.c_int, [_c_ptr, _c_ptr, _c_int, _c_i64, _c_int, _c_int, _c_int, _c_ptr,
+                                      _c_i64, _c_ptr]),
 }
 
 _lock = threading.Lock()

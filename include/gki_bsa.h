@@ -42,11 +42,11 @@
 extern "C" {
 #endif
 
-/* ABI version (currently 7: grouped-query attention, H_kv after H; dK/dV work
+/* ABI version (currently 8: grouped-query attention, H_kv after H; dK/dV work
  * items from gki_dkdv_items, whose chunk can be capped by max_chunk; the
  * optional workgroup orders of the forward and dQ grids from gki_fwd_order;
  * natural-log LSE in every output; gki_bsa_bwd's row-term workspace holds
- * 2 * B * H * N_Q floats). */
+ * 2 * B * H * N_Q floats; the gki_read_probe measurement helper). */
 int gki_abi_version(void);
 
 /* Message of the last failing call on this thread. */
@@ -251,6 +251,20 @@ int gki_rolling_decode_noalloc(const void* q, const void* k_cache, const void* v
                                int32_t n_q, int32_t head_dim, int32_t sink_size,
                                int32_t window_size, int32_t ring_size, int64_t length,
                                float softmax_scale, int32_t n_splits, void* stream);
+
+/* Measurement helper, no counterpart in the reference: reads exactly the K and V
+ * bytes a single-position StreamingLLM decode step reads from a full cache --
+ * per (b, kv head) slice of bh slices of n_kv rows of row_bytes (a multiple of
+ * 16) the sink rows 0 .. min(sink_size, n_kv) - 1 and the window rows
+ * max(that, n_kv - window_size) .. n_kv - 1 -- with 16-byte non-temporal loads
+ * and nothing else, XOR-folding them into `out` (gki_read_probe_words(bh)
+ * words; the XOR of all of them is the XOR of every 32-bit word read). For
+ * timing the decode step against the read ceiling of its own access pattern
+ * (bench.py). Asynchronous on `stream`; allocates nothing. */
+int64_t gki_read_probe_words(int32_t bh);
+int gki_read_probe(const void* k, const void* v, int32_t bh, int64_t n_kv, int32_t row_bytes,
+                   int32_t sink_size, int32_t window_size, uint32_t* out, int64_t out_words,
+                   void* stream);
 
 #ifdef __cplusplus
 }

@@ -188,6 +188,16 @@ static void check_rejections() {
   rejected(gki_fwd_order(nullptr, 2, 2, ord), "order, null row_ptr");
   rejected(gki_fwd_order(down, 0, 2, ord), "order, no q tiles");
   rejected(gki_fwd_order(down, 1 << 20, 1 << 12, ord), "order, table too large");
+  // read probe: null, misaligned, row size, output too small
+  uint32_t* up = (uint32_t*)buf;
+  const int64_t need = gki_read_probe_words(1);
+  CHECK(need > 0 && gki_read_probe_words(0) == 0, "read probe words %lld", (long long)need);
+  rejected(gki_read_probe(nullptr, p, 1, 100, 256, 4, 16, up, need, nullptr), "read probe null k");
+  rejected(gki_read_probe(buf + 4, p, 1, 100, 256, 4, 16, up, need, nullptr), "read probe misaligned k");
+  rejected(gki_read_probe(p, p, 1, 100, 24, 4, 16, up, need, nullptr), "read probe row bytes 24");
+  rejected(gki_read_probe(p, p, 1, 100, 256, -1, 16, up, need, nullptr), "read probe negative sink");
+  rejected(gki_read_probe(p, p, 1, 100, 256, 4, 16, up, need - 1, nullptr), "read probe output too small");
+  rejected(gki_read_probe(p, p, 0, 100, 256, 4, 16, up, need, nullptr), "read probe no slices");
 }
 
 static void check_fwd_order(std::mt19937& rng) {

@@ -104,7 +104,7 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(lib, name), f"{name} declared in gki_bsa.h but not exported"
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
     assert set(_lib.SIGNATURES) == set(names)
-    assert lib.gki_abi_version() == _lib.ABI_VERSION == 7
+    assert lib.gki_abi_version() == _lib.ABI_VERSION == 8
 
 
 def test_load_refuses_other_abi_version(monkeypatch):
@@ -114,14 +114,14 @@ def test_load_refuses_other_abi_version(monkeypatch):
     is unusable (sparse_triton_kernel.py:626-630); nothing is bound from it."""
     monkeypatch.setattr(_lib, "_lib", None)
     monkeypatch.setattr(_lib, "_load_error", None)
-    monkeypatch.setattr(_lib, "ABI_VERSION", 6)
-    with pytest.raises(RuntimeError, match=r"C ABI version 7, this binding needs version 6"):
+    monkeypatch.setattr(_lib, "ABI_VERSION", 7)
+    with pytest.raises(RuntimeError, match=r"C ABI version 8, this binding needs version 7"):
         _lib.load()
     assert not _lib.available()
     # the real binding loads again once the expected version matches
     monkeypatch.setattr(_lib, "_load_error", None)
-    monkeypatch.setattr(_lib, "ABI_VERSION", 7)
-    assert _lib.load().gki_abi_version() == 7
+    monkeypatch.setattr(_lib, "ABI_VERSION", 8)
+    assert _lib.load().gki_abi_version() == 8
 
 
 def test_dkdv_work_list_matches_oracle():

@@ -282,3 +282,32 @@ def test_full_cache_decode_computes_the_stream(B, H, H_kv, n_q, n_kv, D, S, W, d
     m2 = mask.clone()
     m2[0, -2] = 0
     assert decode_schedule(m2, n_q, n_kv, 1, 64, True, S, W).ring == 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("bh,n_kv,D,dtype,sink,window", [
+    (3, 1000, 128, torch.bfloat16, 4, 300),
+    (2, 50, 64, torch.float16, 8, 100),          # the window reaches the sinks: every row once
+    (1, 5, 64, torch.float32, 10, 0),            # more sinks than rows, no window
+    (4, 4099, 128, torch.float16, 0, 2048),
+])
+def test_read_probe_reads_exactly_the_decode_rows(bh, n_kv, D, dtype, sink, window):
+    """gki_read_probe (bench.py's read ceiling of the decode step) folds exactly
+    the sink rows and the window rows of every slice: the XOR of its output
+    words is the XOR of those rows' 32-bit words."""
+    lib = _lib.load()
+    gen = torch.Generator().manual_seed(n_kv)
+    k = torch.randn(bh, n_kv, D, generator=gen).to(dtype)
+    v = torch.randn(bh, n_kv, D, generator=gen).to(dtype)
+    words = int(lib.gki_read_probe_words(bh))
+    out = torch.full((words,), -1, dtype=torch.int32, device=DEV)
+    kd, vd = k.to(DEV), v.to(DEV)
+    _lib.check(lib.gki_read_probe(kd.data_ptr(), vd.data_ptr(), bh, n_kv, D * k.element_size(), sink, window,
+                                  out.data_ptr(), words, torch.cuda.current_stream().cuda_stream),
+               "gki_read_probe")
+    n_sink = min(sink, n_kv)
+    w_lo = max(n_sink, n_kv - window)
+    rows = [t[:, :n_sink] for t in (k, v)] + [t[:, w_lo:] for t in (k, v)]
+    want = np.bitwise_xor.reduce(np.concatenate([r.contiguous().view(torch.int32).numpy().ravel()
+                                                 for r in rows] + [np.zeros(1, np.int32)]))
+    assert np.bitwise_xor.reduce(out.cpu().numpy()) == want
