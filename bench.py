@@ -10,7 +10,10 @@ KV GB/s, each as a fraction of the MI355X roofline.
 * ``train``  -- config 3: fwd + bwd, B4 H16 N8192 D64 fp16, S4 W1024
   (fwd 4*BM*BN*D, bwd 10*BM*BN*D per kept tile).
 * ``decode`` -- config 4: B8 H32, one query, KV 100000, D128 bf16, S4 W2048;
-  token-exact kept K/V bytes (S+W)*D*2*2 per (b, h) over the step time.
+  token-exact kept K/V bytes (S+W)*D*2*2 per (b, h) over the step time; also
+  with the memory-side cache evicted, beside a plain read of exactly the same
+  rows (``read_ceiling``), and the grouped-query / multi-query /
+  four-position variants of the step.
 * ``layer_c5`` -- one config-5 attention layer (1x16x131072x64 bf16, S4 W4096,
   128x64 blocks), fwd + bwd.
 * ``cpu_baseline`` -- the reference's eager masked attention (restated in
