@@ -298,12 +298,10 @@ def section_c4(steps: int, warmup: int, cpu_sample: Optional[dict] = None) -> di
     return res
 
 
-def _read_ceiling_c4(k, v, S, W, exact_bytes, decode_ms, decode_cold_ms, steps, warmup) -> dict:
-    """The read ceiling of the c4 step's own access pattern: ``gki_read_probe``
-    streams exactly its token-exact K / V rows (the sink rows and the window
-    rows of every (b, h) slice) with 16-byte non-temporal loads and no other
-    work, timed like the step: back to back, and after the 2 GiB read that
-    evicts the memory-side cache. ``decode_share`` = probe time / step time."""
+def _read_probe(k, v, S, W):
+    """A call of ``gki_read_probe`` over the rows a one-position decode step
+    reads from K / V ``[B, H_kv, n_kv, D]``: the sink rows and window rows of
+    every (b, kv head) slice."""
     import torch
 
     from gki import _lib
@@ -320,6 +318,16 @@ def _read_ceiling_c4(k, v, S, W, exact_bytes, decode_ms, decode_cold_ms, steps, 
         _lib.check(lib.gki_read_probe(k.data_ptr(), v.data_ptr(), bh, NKV, row_bytes, S, W, out.data_ptr(),
                                       words, stream), "gki_read_probe")
 
+    return fn
+
+
+def _read_ceiling_c4(k, v, S, W, exact_bytes, decode_ms, decode_cold_ms, steps, warmup) -> dict:
+    """The read ceiling of the c4 step's own access pattern: ``gki_read_probe``
+    streams exactly its token-exact K / V rows (the sink rows and the window
+    rows of every (b, h) slice) with 16-byte non-temporal loads and no other
+    work, timed like the step: back to back, and after the 2 GiB read that
+    evicts the memory-side cache. ``decode_share`` = probe time / step time."""
+    fn = _read_probe(k, v, S, W)
     avg, _ = _time_calls(fn, steps, warmup)
     cold = _time_cold(fn)
     res = {"protocol": "gki_read_probe over the same token-exact rows (8 chunks x 256 threads x 4 "
@@ -359,10 +367,16 @@ def _gqa_c4(B, H, NKV, D, S, W, mask, steps, warmup, H_kv=8, n_q=1) -> dict:
     avg, per = _time_calls(fn, steps, warmup)
     kv_bytes = (S + W + n_q - 1) * D * 2 * 2 * B * H_kv
     gbs = kv_bytes / (avg * 1e-3) / 1e9
+    res = {"workload": f"c4 with H {H}, H_kv {H_kv}, n_q {n_q}", "kv_bytes_token_exact": kv_bytes,
+           "avg_ms": avg, "p50_ms": statistics.median(per), "kv_gbs": gbs}
+    extra = ""
+    if n_q == 1:      # the plain read of the same rows, back to back (decode.read_ceiling's probe)
+        probe, _ = _time_calls(_read_probe(k, v, S, W), steps, warmup)
+        res["read_ceiling_ms"], res["decode_share"] = probe, probe / avg
+        extra = f"; a plain read of its rows takes {probe * 1e3:.2f} us ({100 * probe / avg:.0f}% of the step)"
     log(f"[c4] H{H}/H_kv{H_kv} n_q {n_q}: decode step {avg * 1e3:.2f} us, {gbs:.0f} GB/s token-exact "
-        f"({kv_bytes / 1e6:.0f} MB of K/V)")
-    return {"workload": f"c4 with H {H}, H_kv {H_kv}, n_q {n_q}", "kv_bytes_token_exact": kv_bytes,
-            "avg_ms": avg, "p50_ms": statistics.median(per), "kv_gbs": gbs}
+        f"({kv_bytes / 1e6:.0f} MB of K/V){extra}")
+    return res
 
 
 def _rolling_c4(q, k, v, S, W, o_full, exact_bytes, steps, warmup) -> dict:
