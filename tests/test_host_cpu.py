@@ -107,6 +107,17 @@ def test_library_exports_every_declared_symbol():
     assert lib.gki_abi_version() == _lib.ABI_VERSION == 8
 
 
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    """Without the built gfx950 library the binding raises, naming the build
+    command and that there is no CPU fallback; nothing is bound."""
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "_load_error", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "libgki_bsa.so")
+    with pytest.raises(RuntimeError, match=r"unavailable \(OSError.*no CPU fallback"):
+        _lib.load()
+    assert not _lib.available()
+
+
 def test_load_refuses_other_abi_version(monkeypatch):
     """A library whose gki_abi_version differs from the binding's table (a stale
     build exporting the same names with other argument lists) is refused with a
