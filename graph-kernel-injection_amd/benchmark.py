@@ -308,7 +308,10 @@ def verdict(ours: BenchResult, flex: Optional[BenchResult], flex_error: Optional
 
 
 def run_benchmark(cfg: HarnessConfig, csv_path: Optional[Path] = None,
-                  backward: bool = True) -> List[BenchResult]:
+                  backward: bool = True, skip: Sequence[str] = ()) -> List[BenchResult]:
+    """Time every method at ``cfg`` (the methods in ``skip`` are left out: a
+    dense baseline at a long sequence can take minutes per call); each
+    method's times are printed as soon as they are measured."""
     if not torch.cuda.is_available():
         raise RuntimeError("benchmark.py needs a GPU")
     mask = _make_mask(cfg)
@@ -325,6 +328,10 @@ def run_benchmark(cfg: HarnessConfig, csv_path: Optional[Path] = None,
     results: List[BenchResult] = []
     failures: Dict[str, str] = {}
     for label, f_fwd in fwd_fns.items():
+        if label in skip:
+            print(f"[skip] {label}: left out (--skip)", flush=True)
+            failures[label] = "left out (--skip)"
+            continue
         if f_fwd is None:
             print(f"[skip] {label}: not applicable at this shape / unavailable", flush=True)
             failures[label] = "not applicable at this shape / unavailable"
@@ -368,6 +375,9 @@ def run_benchmark(cfg: HarnessConfig, csv_path: Optional[Path] = None,
         results.append(BenchResult(label, str(cfg.dtype).replace("torch.", ""), cfg.seq_len_kv,
                                    density, statistics.median(lat), percentile(lat, 95), p50_b,
                                    p95_b, peak, errors.get(label)))
+        r = results[-1]
+        both = "" if p50_b is None else f", fwd+bwd p50 {p50_b:.3f} / p95 {p95_b:.3f} ms"
+        print(f"[time] {label}: fwd p50 {r.fwd_p50_ms:.3f} / p95 {r.fwd_p95_ms:.3f} ms{both}", flush=True)
         torch.cuda.empty_cache()
     widths = [max(len(h), *(len(r.row()[i]) for r in results)) for i, h in enumerate(HEADERS)]
     print("  ".join(h.ljust(w) for h, w in zip(HEADERS, widths)))
@@ -404,6 +414,9 @@ def _parse(argv: Optional[Sequence[str]] = None) -> argparse.Namespace:
     p.add_argument("--iters", type=int, default=100)
     p.add_argument("--no-backward", action="store_true", help="time the forward only")
     p.add_argument("--csv", type=Path, default=None)
+    p.add_argument("--skip", action="append", default=[], metavar="METHOD",
+                   choices=["flex-attention", "sdpa-explicit-mask", "sdpa-causal-dense", "eager-dense"],
+                   help="leave a comparison method out (repeatable)")
     return p.parse_args(argv)
 
 
@@ -414,7 +427,7 @@ def main(argv: Optional[Sequence[str]] = None) -> int:
                         head_dim=a.head_dim, block_m=min(a.block_m, a.seq_q), block_n=a.block_n,
                         sink_size=a.sink, window_size=a.window, dtype=dtype,
                         warmup_iters=a.warmup, measure_iters=a.iters)
-    run_benchmark(cfg, a.csv, backward=not a.no_backward)
+    run_benchmark(cfg, a.csv, backward=not a.no_backward, skip=a.skip)
     return 0
 
 

@@ -5,6 +5,7 @@ docs/eval_plan.md §5, the scaled-down error shape (benchmark.py:633-648)."""
 from __future__ import annotations
 
 import numpy as np
+import pytest
 import torch
 
 import benchmark as bm
@@ -51,3 +52,11 @@ def test_failure_text_keeps_first_line_and_the_cause():
     assert bm.failure_text(RuntimeError("one line")) == "RuntimeError: one line"
     assert bm.failure_text(RuntimeError("first\nno cause here")) == "RuntimeError: first"
     assert bm.failure_text(RuntimeError()) == "RuntimeError"
+
+
+def test_skip_option_names_comparison_methods_only():
+    a = bm._parse(["--skip", "sdpa-causal-dense", "--skip", "eager-dense"])
+    assert a.skip == ["sdpa-causal-dense", "eager-dense"]
+    assert bm._parse([]).skip == []
+    with pytest.raises(SystemExit):
+        bm._parse(["--skip", bm.OURS])   # this build is always timed
