@@ -303,27 +303,41 @@ def dkdv_items(col_ptr_host: torch.Tensor, group: int, bh_kv: int, max_chunk: in
     return items, split, counts[0].value, counts[1].value, counts[2].value
 
 
+def spread_chunk(col_ptr_host: torch.Tensor, group: int, bh_kv: int, target: int) -> int:
+    """Iterations per dK/dV work item that spread the column walks over about
+    ``target`` items (at least two iterations each) when the ``bh_kv`` x
+    columns are fewer than ``target``; 0 (the library's own chunk) otherwise."""
+    n_cols = (col_ptr_host.numel() - 1) * bh_kv
+    if target <= 0 or n_cols >= target:
+        return 0
+    total = int(col_ptr_host[-1]) * group * bh_kv
+    return max(2, -(-total // target))
+
+
 def bwd_schedule(mask: torch.Tensor, n_q: int, n_kv: int, block_m: int, block_n: int,
                  is_causal: bool, sink: int, window: int, group: int = 1,
-                 bh_kv: int = 1, max_chunk: int = 0) -> BwdSchedule:
+                 bh_kv: int = 1, max_chunk: int = 0, spread_to: int = 0) -> BwdSchedule:
     """CSR + CSC schedules of the dQ and dK/dV kernels (64x64 tiles) and the
     dK/dV work list for ``group`` q heads per kv head over ``bh_kv`` = B * H_kv
-    (b, kv head) pairs (items of at most ``max_chunk`` iterations when positive)."""
+    (b, kv head) pairs (items of at most ``max_chunk`` iterations when positive;
+    with ``spread_to``, short grids are cut into about that many items, see
+    ``spread_chunk``)."""
     ts = _lib.tile_sizes()
     tm, tn = ts["bwd_tile_m"], ts["tile_n"]
 
     def build() -> BwdSchedule:
         tiles = tile_matrix(mask, n_q, n_kv, block_m, block_n, tm, tn, is_causal, sink, window)
         lists = _lists_of(tiles)
-        items, split, n_items, n_split, n_pslots = dkdv_items(lists.col_ptr.cpu(), group, bh_kv,
-                                                              max_chunk)
+        col_ptr = lists.col_ptr.cpu()
+        chunk = max_chunk or spread_chunk(col_ptr, group, bh_kv, spread_to)
+        items, split, n_items, n_split, n_pslots = dkdv_items(col_ptr, group, bh_kv, chunk)
         dev = mask.device
         dq_order = _grid_order(lists.row_ptr, lists.n_rows, group * bh_kv, dev)
         return BwdSchedule(lists, items.to(dev), n_items, split.to(dev), n_split, n_pslots,
                            lists.n_rows, lists.n_cols, dq_order)
 
     key = ("bwd", n_q, n_kv, block_m, block_n, tm, tn, bool(is_causal), sink, window, group, bh_kv,
-           max_chunk)
+           max_chunk, spread_to)
     return _CACHE.get(mask, key, build)
 
 

@@ -31,6 +31,9 @@ _HEAD_DIMS = (16, 32, 64, 128)
 _DECODE_HEAD_DIMS = (64, 128)
 # decode workgroups to aim for: one 768-thread group on each of the 256 CUs
 _DECODE_TARGET_WGS = 256
+# fp32 dK/dV work items wanted when the kv-tile columns are fewer: the fp32
+# kernel runs one workgroup per CU, two per CU of the 256 keep them all busy
+_FP32_DKDV_TARGET_ITEMS = 512
 
 
 def _aligned(t: torch.Tensor) -> torch.Tensor:
@@ -260,8 +263,10 @@ class _BlockSparseFlashAttention(torch.autograd.Function):
         delta = torch.empty((2, B, H, N_Q), dtype=torch.float32, device=q.device)
         with _on_device(q.device):
             stream = _current_stream(q.device)
+            spread = _FP32_DKDV_TARGET_ITEMS if q.dtype == torch.float32 else 0
             sched = bwd_schedule(block_mask, N_Q, N_KV, ctx.block_m, ctx.block_n, ctx.is_causal,
-                                 ctx.sink_size, ctx.window_size, group=H // H_kv, bh_kv=B * H_kv)
+                                 ctx.sink_size, ctx.window_size, group=H // H_kv, bh_kv=B * H_kv,
+                                 spread_to=spread)
             L = sched.lists
             # fp32 dK / dV partials of the split kv tiles: [B*H_kv, n_pslots, 2, 64, D]
             tile_n = _lib.tile_sizes()["tile_n"]

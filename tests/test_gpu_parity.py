@@ -20,6 +20,7 @@ import torch
 import fx_compiler_pass as fxp
 import sparse_triton_kernel as stk
 from gki import _lib, build_block_lists
+from gki.ops import _FP32_DKDV_TARGET_ITEMS
 from gki.lists import bwd_schedule, decode_schedule, fwd_order, fwd_schedule
 from oracle import chunked_reference as cr
 from oracle import streaming_oracle as so
@@ -425,7 +426,9 @@ def _forward_lse(q, k, v, mask, bm, bn, S, W):
                                          (torch.bfloat16, None), (torch.bfloat16, 1 << 20)])
 def test_dkdv_any_cut_of_the_work_list_matches_oracle(chunk, dtype):
     """gki_bsa_bwd through the C ABI with the dK/dV work list cut at any chunk
-    (1 iteration per item, 5, the op's own list, never): every cut gives the
+    (1 iteration per item, 5, the library's default list -- the op's own for
+    16-bit inputs; fp32 ones spread short grids into 2+ iteration items --,
+    never): every cut gives the
     oracle's gradients, grouped-query (4 q heads per kv head) so items also
     split inside a group. Inputs N(0, 1): the sink keys' walk covers 44
     iterations (2816 q rows, |dV| up to ~9). The fp32 kernels add each
@@ -613,7 +616,9 @@ def test_dq_order_gives_the_index_order_bits(dtype):
                                      sink_size=S, window_size=W)
     lse = out.grad_fn.saved_tensors[4]
     out.backward(do)
-    sched = bwd_schedule(mask, N, N, bm, bm, True, S, W, group=1, bh_kv=B * H)   # the op's own
+    spread = _FP32_DKDV_TARGET_ITEMS if dtype == torch.float32 else 0
+    sched = bwd_schedule(mask, N, N, bm, bm, True, S, W, group=1, bh_kv=B * H,
+                         spread_to=spread)   # the op's own
     assert sorted(sched.dq_order.cpu().tolist()) == list(range(sched.n_qt * B * H))
     L = sched.lists
     partials = torch.empty(max(B * H * sched.n_pslots * 2 * 64 * D, 1), dtype=torch.float32, device=DEV)

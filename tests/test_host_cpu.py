@@ -318,3 +318,19 @@ def test_capi_rejects_bad_arguments_before_launch():
     rc = lib.gki_bsa_fwd(16, 16, 16, 16, 16, 2, 1, 1, 1, n, n, 64, 16, 16, 1, 0, 16, n // 16, n // 16, 16,
                          16, 0.1, 1, 4, 8, null)
     assert rc == 1 and b"block mask too large" in lib.gki_last_error()
+
+
+def test_fp32_dkdv_spread_chunk():
+    """Short fp32 grids: the dK/dV column walks are cut so that about ``target``
+    items result, at least two iterations each; grids with enough columns keep
+    the library's own chunk (0)."""
+    from gki.lists import spread_chunk
+
+    def ptr(lens):
+        return torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int32)
+
+    assert spread_chunk(ptr([6] * 16), 1, 4, 512) == 2           # c1: 64 columns of ~6
+    assert spread_chunk(ptr([18] * 64), 1, 4, 512) == 9          # 256 columns of 18
+    assert spread_chunk(ptr([18] * 64), 2, 4, 512) == 18         # q heads per kv head count
+    assert spread_chunk(ptr([18] * 128), 1, 4, 512) == 0         # 512 columns fill the grid
+    assert spread_chunk(ptr([6] * 16), 1, 4, 0) == 0             # not asked for
