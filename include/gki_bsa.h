@@ -107,7 +107,10 @@ int gki_block_list_fill(const int32_t* m, int32_t n_rows, int32_t n_cols,
  * whose fp32 partials gki_bsa_bwd sums in item order (deterministic; fp32
  * partials with a compensated sum). max_chunk > 0 caps the chunk (more,
  * shorter items: a caller may cut columns of any length, as the tests do to
- * run the split path on short sequences); 0 keeps the rule above. Writes
+ * run the split path on short sequences); 0 keeps the rule above. The Python
+ * op passes max(2, ceil(total iterations / 512)) for fp32 inputs whose
+ * B * H_kv * n_kt columns number under 512: the fp32 dK/dV kernel runs one
+ * workgroup per CU, and short grids would leave CUs idle. Writes
  * items [n_items][4] = (kv tile, first iteration, end iteration, partial slot or
  * -1) and split [n_split][3] = (kv tile, first slot, slot count), and the counts;
  * pass items = split = NULL to size them first. n_pslots partial slots per
