@@ -609,7 +609,8 @@ struct DkdvSmem32 {
 // One wave per SIMD from head_dim 64 up: the compensated accumulators, the
 // register-staged next tile and the four MFMA chains then fit in VGPRs + AGPRs
 // (at two waves per SIMD, head_dim 64 spilled 400 bytes per lane: the c1
-// backward ran 25% slower, a B1 H16 N8192 fp32 backward 13% slower).
+// backward took 0.284 against 0.213 ms, a B1 H16 N8192 fp32 backward 2.65
+// against 2.0 ms).
 template <int D>
 __global__ __launch_bounds__(256, D >= 64 ? 1 : 2) void dkdv_kernel_32(
     Geom g, const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
@@ -1106,10 +1107,11 @@ struct DqSmem32 {
   float v[64 * (D + 4)];
 };
 
-// One wave per SIMD from head_dim 64 up, as dkdv_kernel_32 (two spilled 36
-// bytes per lane at head_dim 64, 764 at 128).
+// One wave per SIMD at head_dim 128 (two spilled 764 bytes per lane). At 64
+// two waves spill 36 bytes and still win on full grids (B1 H16 N8192 fp32
+// backward 2.33 -> 1.99 ms against one wave; equal on c1).
 template <int D>
-__global__ __launch_bounds__(256, D >= 64 ? 1 : 2) void dq_kernel_32(
+__global__ __launch_bounds__(256, D >= 128 ? 1 : 2) void dq_kernel_32(
     Geom g, const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ dO, float* __restrict__ dQ, const float* __restrict__ LSE,
     const float* __restrict__ Delta, const int32_t* __restrict__ row_ptr,
