@@ -621,6 +621,9 @@ __global__ __launch_bounds__(256, D >= 64 ? 1 : 2) void dkdv_kernel_32(
   constexpr int KS = D / 4;
   constexpr int DT = D / 16;
   constexpr int LD = D + 4;
+  // the four key subtiles unrolled below head_dim 128; at 128 a rolled loop
+  // keeps the kernel in VGPRs + AGPRs (unrolled it spilled 868 bytes per lane)
+  constexpr int kSubtileUnroll = D >= 128 ? 1 : 4;
   __shared__ __align__(16) DkdvSmem32<D> sm;
   Stage32<D> sq, sdo;
 
@@ -686,7 +689,7 @@ __global__ __launch_bounds__(256, D >= 64 ? 1 : 2) void dkdv_kernel_32(
 
     const bool need_mask = partial || (q0 + kTileM > g.n_q) || (k_w + 15 >= g.n_kv) ||
                            !tile_all_visible(g, q0, min(q0 + kTileM - 1, g.n_q - 1), k_w, kv_hi_wave);
-#pragma unroll
+#pragma unroll kSubtileUnroll
     for (int t = 0; t < 4; ++t) {
       floatx4 fk[DT], fv[DT];          // this subtile's 16 rows, folded in compensated
 #pragma unroll
