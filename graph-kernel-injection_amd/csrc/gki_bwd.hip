@@ -1111,8 +1111,8 @@ struct DqSmem32 {
 };
 
 // One wave per SIMD at head_dim 128 (two spilled 764 bytes per lane). At 64
-// two waves spill 36 bytes and still win on full grids (B1 H16 N8192 fp32
-// backward 2.33 -> 1.99 ms against one wave; equal on c1).
+// two waves win on full grids (B1 H16 N8192 fp32 backward 2.33 -> 1.99 ms
+// against one wave; equal on c1).
 template <int D>
 __global__ __launch_bounds__(256, D >= 128 ? 1 : 2) void dq_kernel_32(
     Geom g, const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
@@ -1122,6 +1122,9 @@ __global__ __launch_bounds__(256, D >= 128 ? 1 : 2) void dq_kernel_32(
   constexpr int KS = D / 4;
   constexpr int DT = D / 16;
   constexpr int LD = D + 4;
+  // the four key subtiles in a rolled loop at head_dim 64: two waves per SIMD
+  // then fit without scratch (209 VGPRs; unrolled, 36 bytes spilled per lane)
+  constexpr int kSubtileUnroll = D == 64 ? 1 : 4;
   __shared__ __align__(16) DqSmem32<D> sm;
   Stage32<D> sk, sv;
 
@@ -1171,7 +1174,7 @@ __global__ __launch_bounds__(256, D >= 128 ? 1 : 2) void dq_kernel_32(
     }
     const bool need_mask = partial || (q0 + 15 >= g.n_q) || (k0 + kTileN > g.n_kv) ||
                            !tile_all_visible(g, q0, q_hi_wave, k0, k0 + kTileN - 1);
-#pragma unroll
+#pragma unroll kSubtileUnroll
     for (int t = 0; t < 4; ++t) {
       floatx4 fq[DT];                  // this subtile's 16 keys, folded in compensated
 #pragma unroll
