@@ -206,6 +206,8 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
   const int BH = g.B * g.H_kv;
   int bh;
   const KvItem item = kv_item_of(blockIdx.x, BH, w, bh);
+  // an empty column (no kept q tile) only writes zeros: its K / V rows are not read
+  const bool has_work = item.it1 > item.it0;
   const int kt = item.kt;
   const size_t kb = (size_t)bh * g.n_kv * D;
   const int bhq0 = (bh / g.H_kv) * g.H + (bh % g.H_kv) * g.group;   // first q head
@@ -218,7 +220,7 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel_16(
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
     const int d0 = 32 * ks + 8 * grp;
-    const bool ok = my_kv < g.n_kv && d0 < D;
+    const bool ok = has_work && my_kv < g.n_kv && d0 < D;
     kf[ks] = ok ? *(const uint4*)(K + kb + (size_t)my_kv * D + d0) : make_uint4(0, 0, 0, 0);
     vf[ks] = ok ? *(const uint4*)(V + kb + (size_t)my_kv * D + d0) : make_uint4(0, 0, 0, 0);
     if constexpr (PRE) vf[ks] = scale8<T>(vf[ks], g.scale);
@@ -395,6 +397,8 @@ __global__ __launch_bounds__(256, 3) void dkdv_kernel_q64(
   const int BH = g.B * g.H_kv;
   int bh;
   const KvItem item = kv_item_of(blockIdx.x, BH, w, bh);
+  // an empty column (no kept q tile) only writes zeros: its K / V rows are not read
+  const bool has_work = item.it1 > item.it0;
   const int kt = item.kt;
   const size_t kb = (size_t)bh * g.n_kv * D;
   const int bhq0 = (bh / g.H_kv) * g.H + (bh % g.H_kv) * g.group;   // first q head
@@ -410,7 +414,7 @@ __global__ __launch_bounds__(256, 3) void dkdv_kernel_q64(
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const int d0 = 32 * ks + 8 * grp;
-      const bool ok = my_kv < g.n_kv;
+      const bool ok = has_work && my_kv < g.n_kv;
       kf[b][ks] = ok ? *(const uint4*)(K + kb + (size_t)my_kv * D + d0) : make_uint4(0, 0, 0, 0);
       vf[b][ks] = ok ? *(const uint4*)(V + kb + (size_t)my_kv * D + d0) : make_uint4(0, 0, 0, 0);
       if constexpr (PRE) vf[b][ks] = scale8<T>(vf[b][ks], g.scale);
@@ -631,6 +635,8 @@ __global__ __launch_bounds__(256, D >= 64 ? 1 : 2) void dkdv_kernel_32(
   const int BH = g.B * g.H_kv;
   int bh;
   const KvItem item = kv_item_of(blockIdx.x, BH, w, bh);
+  // an empty column (no kept q tile) only writes zeros: its K / V rows are not read
+  const bool has_work = item.it1 > item.it0;
   const int kt = item.kt;
   const size_t kb = (size_t)bh * g.n_kv * D;
   const int bhq0 = (bh / g.H_kv) * g.H + (bh % g.H_kv) * g.group;
@@ -642,7 +648,7 @@ __global__ __launch_bounds__(256, D >= 64 ? 1 : 2) void dkdv_kernel_32(
   float kf[KS], vf[KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
-    const bool ok = my_kv < g.n_kv;
+    const bool ok = has_work && my_kv < g.n_kv;
     kf[ks] = ok ? K[kb + (size_t)my_kv * D + 4 * ks + grp] : 0.f;
     vf[ks] = ok ? V[kb + (size_t)my_kv * D + 4 * ks + grp] : 0.f;
   }
